@@ -1,0 +1,214 @@
+/*
+ * m27q.h -- C ABI of the MI355X (gfx950) quantized linear-algebra path.
+ *
+ * Drop-in for the matvec launch layer of mono27b (eramax/mono-qwen27,
+ * src/mono27b_executor.cu, "exec" below).  Every entry point names the
+ * reference interface it replaces.  Conventions:
+ *
+ *  - Plain C types only: device pointers are void* / float*, sizes are ints.
+ *  - Every buffer is caller-owned device memory; nothing here allocates
+ *    device memory.  Scratch space is an explicit argument.
+ *  - Every call validates its arguments on the host before any HIP call and
+ *    returns a status (the reference's launchers silently skip on bad input,
+ *    exec:2034, :2056-2059).
+ *  - Work is enqueued on the given stream; nothing synchronizes, allocates or
+ *    reads device memory on the host, so every device entry point can be
+ *    recorded into a HIP graph.
+ *  - Weights are described by m27q_weight, the reference's WeightView
+ *    (include/mono27b_config.h:63-68) plus a layout tag.
+ */
+#ifndef M27Q_H
+#define M27Q_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define M27Q_API __attribute__((visibility("default")))
+#else
+#define M27Q_API
+#endif
+
+typedef enum m27q_status {
+    M27Q_OK = 0,
+    M27Q_ERR_NULL = 1,        /* a required pointer is NULL */
+    M27Q_ERR_SHAPE = 2,       /* row_blocks / row_count / M / K / n out of range */
+    M27Q_ERR_TYPE = 3,        /* ggml type not supported by this entry point */
+    M27Q_ERR_LAYOUT = 4,      /* unknown layout tag or misaligned buffer */
+    M27Q_ERR_SCRATCH = 5,     /* scratch buffer smaller than required */
+    M27Q_ERR_RANGE = 6,       /* token id out of range, or k > n */
+    M27Q_ERR_HIP = 7          /* the HIP launch itself failed */
+} m27q_status;
+
+/* ggml type ids, as include/mono27b_gguf.h:27-43 numbers them. */
+enum {
+    M27Q_TYPE_F32 = 0,
+    M27Q_TYPE_F16 = 1,
+    M27Q_TYPE_Q8_0 = 8,
+    M27Q_TYPE_Q4_K = 12,
+    M27Q_TYPE_Q6_K = 14
+};
+
+/* Weight layouts in device memory.
+ *  GGUF : rows of raw GGUF blocks, row-major [row_count][row_blocks], exactly as
+ *         the reference uploads them (exec:1695-1716).
+ *  TILED: the pack-time re-tiling produced by m27q_repack.  Rows are grouped in
+ *         tiles of 8; within a tile, each block column is stored plane by plane
+ *         (headers, then quants) so that one wavefront load instruction reads
+ *         1 KiB of contiguous bytes.  Byte-preserving per block, 16-byte aligned,
+ *         inverted exactly by m27q_unpack. */
+enum { M27Q_LAYOUT_GGUF = 0, M27Q_LAYOUT_TILED = 1 };
+
+typedef struct m27q_weight {
+    const void *ptr;        /* device pointer (16-byte aligned for TILED) */
+    uint32_t ggml_type;     /* M27Q_TYPE_* */
+    uint32_t row_blocks;    /* blocks per row (K / block size; K for F16/F32) */
+    uint32_t row_count;     /* rows (N) */
+    uint32_t layout;        /* M27Q_LAYOUT_* */
+} m27q_weight;
+
+M27Q_API const char *m27q_status_string(m27q_status s);
+
+/* ------------------------------------------------------------------------
+ * Host-side, pack time (no GPU needed)
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of one GGUF row of ne elements, 0 if ne is not a whole number of
+ * blocks.  Replaces mono27b_ggml_row_size (src/mono27b_gguf.cpp:375-382). */
+M27Q_API size_t m27q_row_size(uint32_t ggml_type, uint32_t ne);
+
+/* Device bytes a weight occupies in the given layout (TILED pads the row
+ * count to a multiple of 8 and, for Q8_0, the block count to a multiple of 4,
+ * with zero blocks).  0 for an unsupported type/layout. */
+M27Q_API size_t m27q_weight_bytes(uint32_t ggml_type, uint32_t row_blocks, uint32_t row_count,
+                                  uint32_t layout);
+
+/* GGUF rows -> TILED (host memory to host memory).  Replaces the verbatim
+ * copy of lw() (exec:1695-1716) with pack-time re-tiling; the caller uploads
+ * the result.  Supported types: Q4_K, Q6_K, Q8_0. */
+M27Q_API m27q_status m27q_repack(uint32_t ggml_type, uint32_t row_blocks, uint32_t row_count,
+                                 const void *gguf_rows, void *tiled);
+/* TILED -> GGUF rows (the exact inverse of m27q_repack). */
+M27Q_API m27q_status m27q_unpack(uint32_t ggml_type, uint32_t row_blocks, uint32_t row_count,
+                                 const void *tiled, void *gguf_rows);
+
+/* ------------------------------------------------------------------------
+ * Activations
+ * ---------------------------------------------------------------------- */
+
+/* Quantized activation buffer for M rows of K values (K % 32 == 0):
+ *   int8  codes[M][K]             at offset 0
+ *   float d[M][K/32]              at offset m27q_act_d_offset(M, K)
+ *   u32   sums[M][K/32]           at offset m27q_act_s_offset(M, K)
+ * Per 32 values: d = amax/127 (IEEE divide), code = roundf(x/d) clamped to
+ * +-127 (0 when amax == 0), sums = (int16 sum of codes 0..15) |
+ * (int16 sum of codes 16..31) << 16.  The reference's Q8_1 (exec:65-71) keeps
+ * an fp16 d and the float sum of x; this format keeps an fp32 d and the exact
+ * integer sums its dot products use. */
+M27Q_API size_t m27q_act_bytes(int M, int K);
+M27Q_API size_t m27q_act_d_offset(int M, int K);
+M27Q_API size_t m27q_act_s_offset(int M, int K);
+
+/* x[M][K] fp32 -> xq.  Replaces l_quant_q8_n / k_quant_q8_1 (exec:2022-2030,
+ * :84-107). */
+M27Q_API m27q_status m27q_quant_act(const float *x, int M, int K, void *xq, hipStream_t stream);
+
+/* (x * sigmoid(gate)) -> xq.  Replaces k_quant_q8_1_fused_gate (exec:109-138,
+ * site :2460). */
+M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int M, int K, void *xq,
+                                          hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * M = 1 matrix-vector products
+ * ---------------------------------------------------------------------- */
+
+/* y[r] = sum_k W[r][k] * xq[k] (+ residual[r]) on an already-quantized
+ * activation (m27q_quant_act with M = 1 and K = the weight's K).  Q4_K, Q6_K,
+ * Q8_0.  residual may be NULL.  If yq is not NULL, y is also quantized into yq
+ * (format of m27q_quant_act, K = row_count, which must be a multiple of 32):
+ * the fused producer of the next projection's activation.
+ * Replaces l_mv_q8_on (exec:2054-2083) and k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a
+ * / k_q80_mv_q8_dp4a (exec:320-364, :631-645, :535-580) plus the k_elem_add
+ * residual epilogue (exec:2080-2082). */
+M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float *y, const float *residual,
+                                    void *yq, hipStream_t stream);
+
+/* Up to 4 weights that share one activation (same type, layout, row_blocks),
+ * in one launch: y[i] = W[i] xq.  Replaces l_mv_pair (exec:2106-2125) and the
+ * Wq || Wk, Wv pattern of the attention block (exec:2377-2395). */
+M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
+                                          hipStream_t stream);
+
+/* y[r] = silu(Wg xq)[r] * (Wu xq)[r]; both Q4_K/Q6_K/Q8_0 of one shape.  yq as
+ * in m27q_matvec_q8 (may be NULL).  Replaces l_ffn_gate_up_swiglu /
+ * k_q4k_q4k_swiglu_dp4a (exec:2239-2261, :369-417). */
+M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const void *xq,
+                                     float *y, void *yq, hipStream_t stream);
+
+/* fp32-activation product y = W x (+ residual): exact dequantization and fp32
+ * accumulation.  Q4_K, Q6_K, Q8_0, F16, F32.  Replaces l_mv_fallback
+ * (exec:2127-2137) with k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv / k_f32_mv
+ * (exec:920-951, :1053-1072, :1076-1096, :899-916, :1100-1114). */
+M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float *y, const float *residual,
+                                     hipStream_t stream);
+
+/* Quantize x into scratch (>= m27q_act_bytes(1, K) bytes) and run
+ * m27q_matvec_q8; F16/F32 weights go to m27q_matvec_f32.  Replaces l_mv_quant
+ * and l_mv_quant_residual (exec:2033-2050, :2089-2104). */
+M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual,
+                                 void *scratch, size_t scratch_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Small-M products (speculative verify / prefill rows)
+ * ---------------------------------------------------------------------- */
+
+/* Y[m][r] = sum_k W[r][k] * xq[m][k] (+ residual[m][r]) for m < M, 1 <= M <= 64,
+ * xq from m27q_quant_act with this M.  Integer MFMA for M >= 16, packed int8 dot
+ * below.  No reference counterpart: the reference runs prefill and decode one
+ * token at a time (src/mono27b_chat.cpp:399-403); results equal M independent
+ * M = 1 products. */
+M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y,
+                                    const float *residual, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Dequantization, row gather, vocab selection
+ * ---------------------------------------------------------------------- */
+
+/* out[i][:] = dequant(W[row0 + i][:]) for i < nrows, fp32, bit-exact with
+ * ggml's dequantize_row_* (the closed forms of exec:920-951, :1026-1048,
+ * :1076-1096).  Any supported type and layout. */
+M27Q_API m27q_status m27q_dequant_rows(const m27q_weight *w, int row0, int nrows, float *out,
+                                       hipStream_t stream);
+
+/* out[i][:] = dequant(W[ids[i]][:]) for i < n; ids is a device array.  An id
+ * outside [0, row_count) yields a zero row and, if bad_count is not NULL,
+ * increments *bad_count (device int, caller-cleared).  Generalizes
+ * k_q4k_embed (exec:1233-1254), which handles one Q4_K token. */
+M27Q_API m27q_status m27q_embed_rows(const m27q_weight *w, const int32_t *ids, int n, float *out,
+                                     int32_t *bad_count, hipStream_t stream);
+
+/* One token id given on the host; an id outside [0, row_count) returns
+ * M27Q_ERR_RANGE before any launch.  Replaces mono27b_engine_embed
+ * (exec:2641-2664), which writes a zero row for such ids. */
+M27Q_API m27q_status m27q_embed_token(const m27q_weight *w, int32_t token_id, float *out,
+                                      hipStream_t stream);
+
+/* Exact top-k (1 <= k <= 64) of logits[0..n) by (value desc, index asc), -0.0 ==
+ * +0.0, NaN after every number; idx/val are device arrays of k entries, in
+ * rank order.  scratch >= m27q_topk_scratch_bytes(n, k).  Replaces the CPU
+ * candidate selection of sample() (src/mono27b_chat.cpp:211-227) and, with
+ * k = 1, k_argmax / mono27b_engine_argmax (exec:211-239, :2630-2637). */
+M27Q_API size_t m27q_topk_scratch_bytes(int n, int k);
+M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, float *val, void *scratch,
+                               size_t scratch_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* M27Q_H */

@@ -1,0 +1,39 @@
+// m27q_act.hip -- fp32 activations -> per-32 int8 codes with fp32 scale.
+//
+// One lane per value, one 32-lane half-wave per group: amax by cross-lane max,
+// d = amax/127 (IEEE divide), code = roundf(x/d) clamped to +-127, and the two
+// 16-code integer sums.  Replaces k_quant_q8_1 / k_quant_q8_1_fused_gate
+// (exec:84-107, :109-138), which keep an fp16 scale and the float sum of x.
+#include "m27q_internal.h"
+#include "m27q_device.h"
+
+namespace m27q {
+
+template <bool GATED>
+__global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ x, const float *__restrict__ gate,
+                                                   long long n, int8_t *__restrict__ q, float *__restrict__ d,
+                                                   uint32_t *__restrict__ s) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    // n is a multiple of 32, so a 32-lane group is either wholly in range or wholly out.
+    if (i - (threadIdx.x & 31) >= n) return;
+    float v = x[i];
+    if constexpr (GATED) v = v * (1.0f / (1.0f + expf(-gate[i])));
+    float dd;
+    uint32_t ss;
+    const int code = quant32(v, &dd, &ss);
+    q[i] = (int8_t)code;
+    if ((threadIdx.x & 31) == 0) {
+        d[i / 32] = dd;
+        s[i / 32] = ss;
+    }
+}
+
+hipError_t launch_quant_act(const float *x, const float *gate, long long n, int8_t *q, float *d, uint32_t *s,
+                            hipStream_t st) {
+    const int grid = (int)((n + 255) / 256);
+    if (gate) hipLaunchKernelGGL((k_quant_act<true>), dim3(grid), dim3(256), 0, st, x, gate, n, q, d, s);
+    else hipLaunchKernelGGL((k_quant_act<false>), dim3(grid), dim3(256), 0, st, x, gate, n, q, d, s);
+    return hipGetLastError();
+}
+
+}  // namespace m27q

@@ -1,0 +1,328 @@
+// m27q_api.hip -- extern "C" entry points: argument validation, then launches.
+//
+// Every check runs on the host before the first HIP call, so a bad argument
+// returns a status without touching the device (the reference's launchers
+// return silently instead, exec:2034, :2056-2059).
+#include <climits>
+
+#include "m27q_internal.h"
+
+using namespace m27q;
+
+namespace {
+
+constexpr size_t kActAlign = 256;
+constexpr int kMaxK = 1 << 20;
+constexpr int kMaxM = 64;
+constexpr int kMaxTopK = 64;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// LDS limit of one workgroup on the current device (160 KiB on gfx950).
+size_t lds_limit() {
+    static size_t cached = 0;
+    if (!cached) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+            cached = (size_t)v;
+        else
+            cached = 64 * 1024;
+    }
+    return cached;
+}
+
+int k_of(const m27q_weight *w) { return (int)w->row_blocks * block_elems(w->ggml_type); }
+
+// Shared weight checks.  quant_only: Q4_K / Q6_K / Q8_0 only.
+m27q_status check_weight(const m27q_weight *w, bool quant_only) {
+    if (!w || !w->ptr) return M27Q_ERR_NULL;
+    const uint32_t t = w->ggml_type;
+    if (!block_elems(t)) return M27Q_ERR_TYPE;
+    if (quant_only && !is_quant(t)) return M27Q_ERR_TYPE;
+    if (w->row_blocks == 0 || w->row_count == 0 || w->row_count > (uint32_t)INT_MAX / 2) return M27Q_ERR_SHAPE;
+    if ((long long)w->row_blocks * block_elems(t) > kMaxK) return M27Q_ERR_SHAPE;
+    if (w->layout == M27Q_LAYOUT_TILED) {
+        if (!is_quant(t)) return M27Q_ERR_LAYOUT;
+        if (!aligned(w->ptr, 16)) return M27Q_ERR_LAYOUT;
+    } else if (w->layout == M27Q_LAYOUT_GGUF) {
+        const size_t need = (t == kQ6_K || t == kQ8_0) ? 2 : 16;
+        if (!aligned(w->ptr, need)) return M27Q_ERR_LAYOUT;
+        if (t == kF16 && (w->row_blocks % 8)) return M27Q_ERR_SHAPE;
+        if (t == kF32 && (w->row_blocks % 4)) return M27Q_ERR_SHAPE;
+    } else {
+        return M27Q_ERR_LAYOUT;
+    }
+    return M27Q_OK;
+}
+
+struct ActView {
+    const int8_t *q;
+    const float *d;
+    const uint32_t *s;
+};
+
+ActView act_view(const void *xq, int M, int K) {
+    const uint8_t *b = (const uint8_t *)xq;
+    return {(const int8_t *)b, (const float *)(b + m27q_act_d_offset(M, K)),
+            (const uint32_t *)(b + m27q_act_s_offset(M, K))};
+}
+
+int wg_count(int rows) { return ((rows + kTileRows - 1) / kTileRows + kWavesPerWG - 1) / kWavesPerWG; }
+
+m27q_status hip_status(hipError_t e) { return e == hipSuccess ? M27Q_OK : M27Q_ERR_HIP; }
+
+void fill_q8_common(GemvParams &p, const m27q_weight *w, const void *xq) {
+    p.rb = (int)w->row_blocks;
+    p.upr = units_per_row(w->ggml_type, w->row_blocks);
+    p.K = k_of(w);
+    const ActView a = act_view(xq, 1, p.K);
+    p.xq = a.q;
+    p.xd = a.d;
+    p.xs = a.s;
+}
+
+m27q_status check_out_quant(const m27q_weight *w, const void *yq) {
+    if (!yq) return M27Q_OK;
+    if (!aligned(yq, 16)) return M27Q_ERR_LAYOUT;
+    if (w->row_count % kRowsPerWG) return M27Q_ERR_SHAPE;
+    return M27Q_OK;
+}
+
+void fill_out_quant(GemvParams &p, int rows, void *yq) {
+    if (!yq) return;
+    const ActView a = act_view(yq, 1, rows);
+    p.oq = (int8_t *)a.q;
+    p.od = (float *)a.d;
+    p.os = (uint32_t *)a.s;
+}
+
+}  // namespace
+
+extern "C" {
+
+M27Q_API size_t m27q_act_d_offset(int M, int K) {
+    return align_up((size_t)M * K, kActAlign);
+}
+M27Q_API size_t m27q_act_s_offset(int M, int K) {
+    return m27q_act_d_offset(M, K) + align_up((size_t)M * (K / 32) * 4, kActAlign);
+}
+M27Q_API size_t m27q_act_bytes(int M, int K) {
+    if (M <= 0 || K <= 0 || K % 32) return 0;
+    return m27q_act_s_offset(M, K) + align_up((size_t)M * (K / 32) * 4, kActAlign);
+}
+
+static m27q_status quant_act_impl(const float *x, const float *gate, int M, int K, void *xq, hipStream_t s) {
+    if (!x || !xq) return M27Q_ERR_NULL;
+    if (M <= 0 || M > 1 << 16 || K < 32 || K % 32 || K > kMaxK) return M27Q_ERR_SHAPE;
+    if (!aligned(xq, 16) || !aligned(x, 4)) return M27Q_ERR_LAYOUT;
+    const ActView a = act_view(xq, M, K);
+    return hip_status(launch_quant_act(x, gate, (long long)M * K, (int8_t *)a.q, (float *)a.d, (uint32_t *)a.s, s));
+}
+
+M27Q_API m27q_status m27q_quant_act(const float *x, int M, int K, void *xq, hipStream_t stream) {
+    return quant_act_impl(x, nullptr, M, K, xq, stream);
+}
+
+M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int M, int K, void *xq,
+                                          hipStream_t stream) {
+    if (!gate) return M27Q_ERR_NULL;
+    return quant_act_impl(x, gate, M, K, xq, stream);
+}
+
+M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float *y, const float *residual,
+                                    void *yq, hipStream_t stream) {
+    m27q_status st = check_weight(w, true);
+    if (st != M27Q_OK) return st;
+    if (!xq || !y) return M27Q_ERR_NULL;
+    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    if ((st = check_out_quant(w, yq)) != M27Q_OK) return st;
+    GemvParams p{};
+    fill_q8_common(p, w, xq);
+    if (gemv_q8_lds_bytes(w->ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    const int grid = wg_count((int)w->row_count);
+    p.W[0] = (const uint8_t *)w->ptr;
+    p.y[0] = y;
+    p.res[0] = residual;
+    p.rc[0] = (int)w->row_count;
+    p.wg_start[0] = 0;
+    p.wg_start[1] = grid;
+    p.nmat = 1;
+    fill_out_quant(p, (int)w->row_count, yq);
+    return hip_status(launch_gemv_q8(w->ggml_type, (int)w->layout, false, p, grid, stream));
+}
+
+M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
+                                          hipStream_t stream) {
+    if (!ws || !xq || !ys) return M27Q_ERR_NULL;
+    if (n < 1 || n > kMaxMulti) return M27Q_ERR_SHAPE;
+    for (int i = 0; i < n; ++i) {
+        const m27q_status st = check_weight(&ws[i], true);
+        if (st != M27Q_OK) return st;
+        if (!ys[i]) return M27Q_ERR_NULL;
+        if (ws[i].ggml_type != ws[0].ggml_type) return M27Q_ERR_TYPE;
+        if (ws[i].layout != ws[0].layout) return M27Q_ERR_LAYOUT;
+        if (ws[i].row_blocks != ws[0].row_blocks) return M27Q_ERR_SHAPE;
+    }
+    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    GemvParams p{};
+    fill_q8_common(p, &ws[0], xq);
+    if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    int total = 0;
+    for (int i = 0; i < n; ++i) {
+        p.W[i] = (const uint8_t *)ws[i].ptr;
+        p.y[i] = ys[i];
+        p.rc[i] = (int)ws[i].row_count;
+        p.wg_start[i] = total;
+        total += wg_count((int)ws[i].row_count);
+    }
+    p.wg_start[n] = total;
+    p.nmat = n;
+    return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, false, p, total, stream));
+}
+
+M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,
+                                     void *yq, hipStream_t stream) {
+    m27q_status st = check_weight(gate, true);
+    if (st != M27Q_OK) return st;
+    if ((st = check_weight(up, true)) != M27Q_OK) return st;
+    if (!xq || !y) return M27Q_ERR_NULL;
+    if (gate->ggml_type != up->ggml_type) return M27Q_ERR_TYPE;
+    if (gate->layout != up->layout) return M27Q_ERR_LAYOUT;
+    if (gate->row_blocks != up->row_blocks || gate->row_count != up->row_count) return M27Q_ERR_SHAPE;
+    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    if ((st = check_out_quant(gate, yq)) != M27Q_OK) return st;
+    GemvParams p{};
+    fill_q8_common(p, gate, xq);
+    if (gemv_q8_lds_bytes(gate->ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    const int grid = wg_count((int)gate->row_count);
+    p.W[0] = (const uint8_t *)gate->ptr;
+    p.W[1] = (const uint8_t *)up->ptr;
+    p.y[0] = y;
+    p.rc[0] = (int)gate->row_count;
+    p.wg_start[1] = grid;
+    p.nmat = 1;
+    fill_out_quant(p, (int)gate->row_count, yq);
+    return hip_status(launch_gemv_q8(gate->ggml_type, (int)gate->layout, true, p, grid, stream));
+}
+
+M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float *y, const float *residual,
+                                     hipStream_t stream) {
+    const m27q_status st = check_weight(w, false);
+    if (st != M27Q_OK) return st;
+    if (!x || !y) return M27Q_ERR_NULL;
+    if (!aligned(x, 16)) return M27Q_ERR_LAYOUT;
+    GemvParams p{};
+    p.rb = (int)w->row_blocks;
+    p.K = k_of(w);
+    p.upr = is_quant(w->ggml_type) ? units_per_row(w->ggml_type, w->row_blocks) : 0;
+    if (is_quant(w->ggml_type) && gemv_f32_lds_bytes(w->ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    p.x = x;
+    p.W[0] = (const uint8_t *)w->ptr;
+    p.y[0] = y;
+    p.res[0] = residual;
+    p.rc[0] = (int)w->row_count;
+    p.nmat = 1;
+    const int grid = wg_count((int)w->row_count);
+    p.wg_start[1] = grid;
+    return hip_status(launch_gemv_f32(w->ggml_type, (int)w->layout, p, grid, stream));
+}
+
+M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual,
+                                 void *scratch, size_t scratch_bytes, hipStream_t stream) {
+    const m27q_status st = check_weight(w, false);
+    if (st != M27Q_OK) return st;
+    if (!is_quant(w->ggml_type)) return m27q_matvec_f32(w, x, y, residual, stream);
+    if (!x || !y || !scratch) return M27Q_ERR_NULL;
+    const int K = k_of(w);
+    if (scratch_bytes < m27q_act_bytes(1, K)) return M27Q_ERR_SCRATCH;
+    if (!aligned(scratch, 16)) return M27Q_ERR_LAYOUT;
+    const m27q_status q = m27q_quant_act(x, 1, K, scratch, stream);
+    if (q != M27Q_OK) return q;
+    return m27q_matvec_q8(w, scratch, y, residual, nullptr, stream);
+}
+
+M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y, const float *residual,
+                                    hipStream_t stream) {
+    const m27q_status st = check_weight(w, true);
+    if (st != M27Q_OK) return st;
+    if (!xq || !Y) return M27Q_ERR_NULL;
+    if (M < 1 || M > kMaxM) return M27Q_ERR_SHAPE;
+    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    MatmulParams p{};
+    p.W = (const uint8_t *)w->ptr;
+    p.rb = (int)w->row_blocks;
+    p.rc = (int)w->row_count;
+    p.upr = units_per_row(w->ggml_type, w->row_blocks);
+    p.K = k_of(w);
+    p.M = M;
+    const ActView a = act_view(xq, M, p.K);
+    p.xq = a.q;
+    p.xd = a.d;
+    p.xs = a.s;
+    p.Y = Y;
+    p.res = residual;
+    return hip_status(launch_matmul_q8(w->ggml_type, (int)w->layout, p, stream));
+}
+
+static m27q_status gather_impl(const m27q_weight *w, const int32_t *ids, int row0, int n, float *out,
+                               int32_t *bad, hipStream_t stream) {
+    const m27q_status st = check_weight(w, false);
+    if (st != M27Q_OK) return st;
+    if (!out) return M27Q_ERR_NULL;
+    if (!aligned(out, 16)) return M27Q_ERR_LAYOUT;
+    if (n < 1 || n > 65535) return M27Q_ERR_SHAPE;
+    GatherParams p{};
+    p.W = (const uint8_t *)w->ptr;
+    p.type = w->ggml_type;
+    p.layout = (int)w->layout;
+    p.rb = (int)w->row_blocks;
+    p.rc = (int)w->row_count;
+    p.upr = is_quant(w->ggml_type) ? units_per_row(w->ggml_type, w->row_blocks) : 0;
+    p.ids = ids;
+    p.row0 = row0;
+    p.n = n;
+    p.out = out;
+    p.bad = bad;
+    return hip_status(launch_gather(p, stream));
+}
+
+M27Q_API m27q_status m27q_dequant_rows(const m27q_weight *w, int row0, int nrows, float *out, hipStream_t stream) {
+    const m27q_status st = check_weight(w, false);
+    if (st != M27Q_OK) return st;
+    if (row0 < 0 || nrows < 1 || (long long)row0 + nrows > (long long)w->row_count) return M27Q_ERR_RANGE;
+    return gather_impl(w, nullptr, row0, nrows, out, nullptr, stream);
+}
+
+M27Q_API m27q_status m27q_embed_rows(const m27q_weight *w, const int32_t *ids, int n, float *out, int32_t *bad_count,
+                                     hipStream_t stream) {
+    if (!ids) return M27Q_ERR_NULL;
+    if (bad_count && !aligned(bad_count, 4)) return M27Q_ERR_LAYOUT;
+    return gather_impl(w, ids, 0, n, out, bad_count, stream);
+}
+
+M27Q_API m27q_status m27q_embed_token(const m27q_weight *w, int32_t token_id, float *out, hipStream_t stream) {
+    const m27q_status st = check_weight(w, false);
+    if (st != M27Q_OK) return st;
+    if (token_id < 0 || (uint32_t)token_id >= w->row_count) return M27Q_ERR_RANGE;
+    return gather_impl(w, nullptr, token_id, 1, out, nullptr, stream);
+}
+
+M27Q_API size_t m27q_topk_scratch_bytes(int n, int k) {
+    if (n <= 0 || k < 1 || k > kMaxTopK || k > n) return 0;
+    return topk_scratch_bytes(n);
+}
+
+M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, float *val, void *scratch,
+                               size_t scratch_bytes, hipStream_t stream) {
+    if (!logits || !idx || !val || !scratch) return M27Q_ERR_NULL;
+    if (n <= 0) return M27Q_ERR_SHAPE;
+    if (k < 1 || k > kMaxTopK || k > n) return M27Q_ERR_RANGE;
+    if (scratch_bytes < topk_scratch_bytes(n)) return M27Q_ERR_SCRATCH;
+    if (!aligned(scratch, 8)) return M27Q_ERR_LAYOUT;
+    return hip_status(launch_topk(logits, n, k, idx, val, scratch, stream));
+}
+
+}  // extern "C"

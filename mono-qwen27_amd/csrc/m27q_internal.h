@@ -1,0 +1,73 @@
+// m27q_internal.h -- kernel launch interface between the C ABI and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/m27q.h"
+#include "m27q_layout.h"
+
+namespace m27q {
+
+constexpr int kMaxMulti = 4;  // weights sharing one activation in one launch
+
+struct GemvParams {
+    const uint8_t *W[kMaxMulti];
+    float *y[kMaxMulti];
+    const float *res[kMaxMulti];
+    int rc[kMaxMulti];
+    int wg_start[kMaxMulti + 1];  // first workgroup of each weight
+    int nmat;
+    int rb;   // GGUF blocks per row (K elements for F16 / F32)
+    int upr;  // layout units per row
+    int K;    // activation length
+    // int8 activation (m27q_quant_act format) ...
+    const int8_t *xq;
+    const float *xd;
+    const uint32_t *xs;
+    // ... or fp32 activation
+    const float *x;
+    // optional fused quantization of the output vector
+    int8_t *oq;
+    float *od;
+    uint32_t *os;
+};
+
+size_t gemv_q8_lds_bytes(uint32_t type, int upr);
+size_t gemv_f32_lds_bytes(uint32_t type, int upr);
+hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, const GemvParams &p, int grid, hipStream_t s);
+hipError_t launch_gemv_f32(uint32_t type, int layout, const GemvParams &p, int grid, hipStream_t s);
+
+hipError_t launch_quant_act(const float *x, const float *gate, long long n, int8_t *q, float *d, uint32_t *s,
+                            hipStream_t st);
+
+struct GatherParams {
+    const uint8_t *W;
+    uint32_t type;
+    int layout;
+    int rb, rc, upr;
+    const int32_t *ids;  // device ids, or NULL: rows row0 + i
+    int row0;
+    int n;
+    float *out;
+    int32_t *bad;
+};
+hipError_t launch_gather(const GatherParams &p, hipStream_t s);
+
+size_t topk_scratch_bytes(int n);
+hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, void *scratch, hipStream_t s);
+
+struct MatmulParams {
+    const uint8_t *W;
+    int rb, rc, upr, K, M;
+    const int8_t *xq;
+    const float *xd;
+    const uint32_t *xs;
+    float *Y;
+    const float *res;
+};
+hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s);
+
+}  // namespace m27q

@@ -1,0 +1,299 @@
+// m27q_types.h -- per-type lane fragments for the gfx950 GEMV kernels.
+//
+// Work mapping shared by every GEMV kernel: a wavefront owns a tile of 8 rows;
+// lane = 8 * i + c works on row i and on the c-th 16-byte chunk of that row's
+// quants in the current unit (one 256-weight block for Q4_K / Q6_K, four
+// 32-weight blocks for Q8_0).  One unit of 8 rows is therefore read by one
+// 16-byte-per-lane load per plane: 1 KiB of contiguous bytes per instruction
+// in the TILED layout.
+//
+// Activations are staged in LDS by the calling kernel:
+//   int8  xc[Kp]       codes (Kp = K padded to whole units, pad = 0)
+//   float xd[Kp/32]    per-32 scale
+//   u32   xs[Kp/32]    per-type auxiliary word (see stage_aux)
+// and, for the fp32-activation kernels:
+//   float xf[Kp]       values
+//   float x16[Kp/16]   per-16 sums of the values
+#pragma once
+
+#include "m27q_device.h"
+
+namespace m27q {
+
+constexpr uint32_t kM4 = 0x0f0f0f0fu;
+
+struct ActLds {
+    const int8_t *xc;
+    const float *xd;
+    const uint32_t *xs;
+};
+
+struct ActLdsF32 {
+    const float *xf;
+    const float *x16;
+};
+
+__device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
+
+// ------------------------------------------------------------------ Q4_K --
+// Chunk c of a block's 128 qs bytes holds qs[16c, 16c+16): with g = c/2 and
+// h = c%2, the low nibbles are weights 64g + 16h + [0,16) (scale pair 2g), the
+// high nibbles weights 64g + 32 + 16h + [0,16) (pair 2g+1)
+// (debug/official_dequant.c:56-62 for the index map).  Lane c also carries
+// the min term of pair j = c for the whole block.
+struct Q4K {
+    static constexpr uint32_t kType = kQ4_K;
+    static constexpr int kUnitElems = 256;
+    static constexpr int kUnitBytes = kQ4KUnit;
+    static constexpr int kBlockBytes = kQ4KBytes;
+
+    struct Frag {
+        uint4 q;  // 16 qs bytes
+        uint4 h;  // d | dmin << 16, scales[0..4), scales[4..8), scales[8..12)
+    };
+
+    struct Lane {
+        int c, g, off, shA, shm;
+        bool gl, cl;
+        __device__ explicit Lane(int c_) : c(c_) {
+            g = c >> 1;
+            off = 64 * g + 16 * (c & 1);
+            shA = 16 * (g & 1);
+            shm = 8 * (c & 3);
+            gl = g < 2;
+            cl = c < 4;
+        }
+    };
+
+    __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
+        return {ld_u128(unit + 128 + 128 * i + 16 * c), ld_u128(unit + 16 * i)};
+    }
+    __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
+        const uint8_t *blk = row + (size_t)u * kQ4KBytes;
+        return {ld_u128(blk + kQ4KHdr + 16 * c), ld_u128(blk)};
+    }
+
+    // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c:
+    // get_scale_min_k4 (exec:690-693) evaluated on the packed dwords directly.
+    __device__ static uint32_t scale_pair(const uint4 &h, const Lane &L) {
+        return L.gl ? ((h.y >> L.shA) & 0x3f3fu)
+                    : (((h.w >> L.shA) & 0x0f0fu) | ((h.y >> (L.shA + 2)) & 0x3030u));
+    }
+    __device__ static int min_c(const uint4 &h, const Lane &L) {
+        return (int)(L.cl ? ((h.z >> L.shm) & 63u)
+                          : (((h.w >> (L.shm + 4)) & 15u) | ((h.z >> (L.shm + 2)) & 0x30u)));
+    }
+
+    // LDS aux word: d * (sum of the 32 codes), the scale of the block-min term.
+    __device__ static uint32_t stage_aux(float d, uint32_t s) {
+        const int S = (int)(int16_t)(s & 0xffffu) + (int)(int16_t)(s >> 16);
+        return __float_as_uint(d * (float)S);
+    }
+
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        const int4 alo = *(const int4 *)(a.xc + 256 * u + L.off);
+        const int4 ahi = *(const int4 *)(a.xc + 256 * u + L.off + 32);
+        int slo = dot4((int)(f.q.x & kM4), alo.x, 0);
+        slo = dot4((int)(f.q.y & kM4), alo.y, slo);
+        slo = dot4((int)(f.q.z & kM4), alo.z, slo);
+        slo = dot4((int)(f.q.w & kM4), alo.w, slo);
+        int shi = dot4((int)((f.q.x >> 4) & kM4), ahi.x, 0);
+        shi = dot4((int)((f.q.y >> 4) & kM4), ahi.y, shi);
+        shi = dot4((int)((f.q.z >> 4) & kM4), ahi.z, shi);
+        shi = dot4((int)((f.q.w >> 4) & kM4), ahi.w, shi);
+        const uint32_t pair = scale_pair(f.h, L);
+        const int m = min_c(f.h, L);
+        const float2 dx = *(const float2 *)(a.xd + 8 * u + 2 * L.g);
+        const float dsum = __uint_as_float(a.xs[8 * u + L.c]);
+        const float dw = f16_bits_to_f32(f.h.x), dm = f16_bits_to_f32(f.h.x >> 16);
+        const float t = dx.x * (float)((int)(pair & 0xffu) * slo) + dx.y * (float)((int)(pair >> 8) * shi);
+        return dw * t - dm * ((float)m * dsum);
+    }
+
+    __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
+        const float4 *xl = (const float4 *)(a.xf + 256 * u + L.off);
+        const float4 *xh = (const float4 *)(a.xf + 256 * u + L.off + 32);
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        float flo = 0.f, fhi = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = qw[k] & kM4, hi = (qw[k] >> 4) & kM4;
+            const float4 vl = xl[k], vh = xh[k];
+            flo += ubyte_f(lo, 0) * vl.x + ubyte_f(lo, 1) * vl.y + ubyte_f(lo, 2) * vl.z + ubyte_f(lo, 3) * vl.w;
+            fhi += ubyte_f(hi, 0) * vh.x + ubyte_f(hi, 1) * vh.y + ubyte_f(hi, 2) * vh.z + ubyte_f(hi, 3) * vh.w;
+        }
+        const uint32_t pair = scale_pair(f.h, L);
+        const int m = min_c(f.h, L);
+        const float xsum = a.x16[16 * u + 2 * L.c] + a.x16[16 * u + 2 * L.c + 1];
+        const float dw = f16_bits_to_f32(f.h.x), dm = f16_bits_to_f32(f.h.x >> 16);
+        return dw * ((float)(pair & 0xffu) * flo + (float)(pair >> 8) * fhi) - dm * ((float)m * xsum);
+    }
+};
+
+// ------------------------------------------------------------------ Q6_K --
+// Chunk c of ql: half hh = c/4, cc = c%4, l0 = 16 (cc%2), r = cc/2.  Low
+// nibbles are q_r at positions 128hh + 32r + l0 + [0,16), high nibbles q_{r+2}
+// at +64; their top two bits are bits 2r / 2r+4 of qh[32hh + l0 + [0,16)], and
+// their scales are scales[8hh + cc] / scales[8hh + 4 + cc]
+// (exec:1026-1048 for the index map).
+struct Q6K {
+    static constexpr uint32_t kType = kQ6_K;
+    static constexpr int kUnitElems = 256;
+    static constexpr int kUnitBytes = kQ6KUnit;
+    static constexpr int kBlockBytes = kQ6KBytes;
+
+    struct Frag {
+        uint4 ql, qh;
+        uint2 sc;    // scales[8hh .. 8hh+8)
+        uint32_t d;  // f16 bits
+    };
+
+    struct Lane {
+        int hh, cc, qh_off, aoff, jlo, shl_lo, shr_hi;
+        bool hsel;
+        __device__ explicit Lane(int c) {
+            hh = c >> 2;
+            cc = c & 3;
+            const int r = cc >> 1, l0 = 16 * (cc & 1);
+            qh_off = 32 * hh + l0;
+            aoff = 128 * hh + 32 * r + l0;
+            jlo = 4 * hh + r;
+            shl_lo = 4 - 2 * r;
+            shr_hi = 2 * (r + 2) - 4;
+            hsel = (cc & 1) != 0;
+        }
+    };
+
+    __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &L) {
+        Frag f;
+        f.ql = ld_u128(unit + kQ6KTQl + 128 * i + 16 * c);
+        f.qh = ld_u128(unit + kQ6KTQh + 64 * i + L.qh_off);
+        f.sc = *(const uint2 *)(unit + kQ6KTSc + 16 * i + 8 * L.hh);
+        f.d = *(const uint16_t *)(unit + kQ6KTD + 2 * i);
+        return f;
+    }
+    __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &L) {
+        const uint8_t *blk = row + (size_t)u * kQ6KBytes;
+        Frag f;
+        f.ql = ld_u128_a2(blk + kQ6KQl + 16 * c);
+        f.qh = ld_u128_a2(blk + kQ6KQh + L.qh_off);
+        f.sc = make_uint2(ld_u32_a2(blk + kQ6KSc + 8 * L.hh), ld_u32_a2(blk + kQ6KSc + 8 * L.hh + 4));
+        f.d = *(const uint16_t *)(blk + kQ6KD);
+        return f;
+    }
+
+    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }
+
+    __device__ static void codes(const Frag &f, const Lane &L, uint32_t lo6[4], uint32_t hi6[4]) {
+        const uint32_t qlw[4] = {f.ql.x, f.ql.y, f.ql.z, f.ql.w};
+        const uint32_t qhw[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lo6[k] = (qlw[k] & kM4) | ((qhw[k] << L.shl_lo) & 0x30303030u);
+            hi6[k] = ((qlw[k] >> 4) & kM4) | ((qhw[k] >> L.shr_hi) & 0x30303030u);
+        }
+    }
+
+    __device__ static int s16(uint32_t s, bool hi) {
+        return hi ? (int)(int16_t)(s >> 16) : (int)(int16_t)(s & 0xffffu);
+    }
+
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        uint32_t lo6[4], hi6[4];
+        codes(f, L, lo6, hi6);
+        const int4 alo = *(const int4 *)(a.xc + 256 * u + L.aoff);
+        const int4 ahi = *(const int4 *)(a.xc + 256 * u + L.aoff + 64);
+        int slo = dot4((int)lo6[0], alo.x, 0);
+        slo = dot4((int)lo6[1], alo.y, slo);
+        slo = dot4((int)lo6[2], alo.z, slo);
+        slo = dot4((int)lo6[3], alo.w, slo);
+        int shi = dot4((int)hi6[0], ahi.x, 0);
+        shi = dot4((int)hi6[1], ahi.y, shi);
+        shi = dot4((int)hi6[2], ahi.z, shi);
+        shi = dot4((int)hi6[3], ahi.w, shi);
+        const int jl = 8 * u + L.jlo;
+        slo -= 32 * s16(a.xs[jl], L.hsel);      // codes are q+32: remove the offset exactly
+        shi -= 32 * s16(a.xs[jl + 2], L.hsel);
+        const int sclo = (int)(int8_t)(f.sc.x >> (8 * L.cc));
+        const int schi = (int)(int8_t)(f.sc.y >> (8 * L.cc));
+        const float t = a.xd[jl] * ((float)slo * (float)sclo) + a.xd[jl + 2] * ((float)shi * (float)schi);
+        return f16_bits_to_f32(f.d) * t;
+    }
+
+    __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
+        uint32_t lo6[4], hi6[4];
+        codes(f, L, lo6, hi6);
+        const float4 *xl = (const float4 *)(a.xf + 256 * u + L.aoff);
+        const float4 *xh = (const float4 *)(a.xf + 256 * u + L.aoff + 64);
+        float flo = 0.f, fhi = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 vl = xl[k], vh = xh[k];
+            flo += ubyte_f(lo6[k], 0) * vl.x + ubyte_f(lo6[k], 1) * vl.y + ubyte_f(lo6[k], 2) * vl.z +
+                   ubyte_f(lo6[k], 3) * vl.w;
+            fhi += ubyte_f(hi6[k], 0) * vh.x + ubyte_f(hi6[k], 1) * vh.y + ubyte_f(hi6[k], 2) * vh.z +
+                   ubyte_f(hi6[k], 3) * vh.w;
+        }
+        const int g16 = 16 * u + L.aoff / 16;
+        flo -= 32.f * a.x16[g16];
+        fhi -= 32.f * a.x16[g16 + 4];
+        const float sclo = (float)(int8_t)(f.sc.x >> (8 * L.cc));
+        const float schi = (float)(int8_t)(f.sc.y >> (8 * L.cc));
+        return f16_bits_to_f32(f.d) * (sclo * flo + schi * fhi);
+    }
+};
+
+// ------------------------------------------------------------------ Q8_0 --
+// Unit = 4 blocks of 32.  Lane c: block k = c/2 of the unit, half c%2.
+struct Q80 {
+    static constexpr uint32_t kType = kQ8_0;
+    static constexpr int kUnitElems = 128;
+    static constexpr int kUnitBytes = kQ80Unit;
+    static constexpr int kBlockBytes = kQ80Bytes;
+
+    struct Frag {
+        uint4 q;
+        uint32_t d;
+    };
+
+    struct Lane {
+        int k, hf;
+        __device__ explicit Lane(int c) : k(c >> 1), hf(c & 1) {}
+    };
+
+    __device__ static Frag load_tiled(const uint8_t *unit, int i, int /*c*/, const Lane &L) {
+        return {ld_u128(unit + 128 * i + 32 * L.k + 16 * L.hf), *(const uint16_t *)(unit + kQ80TD + 8 * i + 2 * L.k)};
+    }
+    __device__ static Frag load_gguf(const uint8_t *row, int u, int rb, int /*c*/, const Lane &L) {
+        const int bi = 4 * u + L.k;
+        if (bi >= rb) return {make_uint4(0, 0, 0, 0), 0u};
+        const uint8_t *blk = row + (size_t)bi * kQ80Bytes;
+        return {ld_u128_a2(blk + 2 + 16 * L.hf), *(const uint16_t *)blk};
+    }
+
+    __device__ static uint32_t stage_aux(float, uint32_t) { return 0u; }
+
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        const int4 x = *(const int4 *)(a.xc + 128 * u + 32 * L.k + 16 * L.hf);
+        int s = dot4((int)f.q.x, x.x, 0);
+        s = dot4((int)f.q.y, x.y, s);
+        s = dot4((int)f.q.z, x.z, s);
+        s = dot4((int)f.q.w, x.w, s);
+        return f16_bits_to_f32(f.d) * (a.xd[4 * u + L.k] * (float)s);
+    }
+
+    __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
+        const float4 *x = (const float4 *)(a.xf + 128 * u + 32 * L.k + 16 * L.hf);
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 v = x[k];
+            acc += (float)(int8_t)(qw[k]) * v.x + (float)(int8_t)(qw[k] >> 8) * v.y +
+                   (float)(int8_t)(qw[k] >> 16) * v.z + (float)(int8_t)(qw[k] >> 24) * v.w;
+        }
+        return f16_bits_to_f32(f.d) * acc;
+    }
+};
+
+}  // namespace m27q

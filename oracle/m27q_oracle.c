@@ -1,0 +1,714 @@
+/*
+ * m27q_oracle.c -- CPU oracle for the quantized linear-algebra path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker; see m27q_oracle.h for the pins).
+ * Reference = eramax/mono-qwen27; "exec" = src/mono27b_executor.cu.
+ * Built with -ffp-contract=off so every expression rounds as written.
+ */
+#include "m27q_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+size_t ora_type_size(int type) {
+    /* src/mono27b_gguf.cpp:167-180 */
+    switch (type) {
+        case ORA_F32: return 4;
+        case ORA_F16: return 2;
+        case ORA_Q8_0: return 34;
+        case ORA_Q4_K: return 144;
+        case ORA_Q6_K: return 210;
+        case ORA_Q8_K: return 292;
+        default: return 0;
+    }
+}
+
+int ora_block_elems(int type) {
+    /* src/mono27b_gguf.cpp:182-195 */
+    switch (type) {
+        case ORA_F32: case ORA_F16: return 1;
+        case ORA_Q8_0: return 32;
+        case ORA_Q4_K: case ORA_Q6_K: case ORA_Q8_K: return 256;
+        default: return 0;
+    }
+}
+
+/* ---------------------------------------------------------------- fp16 -- */
+
+/* IEEE binary16 -> binary32 from the definition (sign, 5-bit exponent with
+ * bias 15, 10-bit fraction; subnormals scale by 2^-24).  Exact for every
+ * input.  Follows the semantics of ggml_compute_fp16_to_fp32
+ * (debug/official_dequant.c:19-36), written from the format definition. */
+float ora_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t ex = (h >> 10) & 0x1f;
+    const uint32_t fr = h & 0x3ff;
+    uint32_t bits;
+    if (ex == 0x1f) {
+        bits = sign | 0x7f800000u | (fr << 13);              /* inf / nan (payload kept) */
+    } else if (ex != 0) {
+        bits = sign | ((ex + 112u) << 23) | (fr << 13);      /* normal: rebias 15 -> 127 */
+    } else {
+        const float mag = (float)fr * 0x1p-24f;              /* subnormal or zero: exact */
+        union { float f; uint32_t u; } t = { mag };
+        bits = sign | t.u;
+    }
+    union { uint32_t u; float f; } o = { bits };
+    return o.f;
+}
+
+/* binary32 -> binary16, round to nearest even, overflow to inf, nan kept nan. */
+uint16_t ora_fp32_to_fp16(float f) {
+    union { float f; uint32_t u; } in = { f };
+    const uint32_t u = in.u;
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000);
+    const uint32_t ex = (u >> 23) & 0xff;
+    uint32_t man = u & 0x7fffff;
+    if (ex == 0xff) return (uint16_t)(sign | 0x7c00 | (man ? 0x200 | (man >> 13) : 0));
+    const int e = (int)ex - 127;
+    if (e > 15) return (uint16_t)(sign | 0x7c00);
+    if (e >= -14) {
+        /* normal half: keep 10 fraction bits, round the 13 dropped bits */
+        uint32_t h = ((uint32_t)(e + 15) << 10) | (man >> 13);
+        const uint32_t rem = man & 0x1fff;
+        if (rem > 0x1000 || (rem == 0x1000 && (h & 1))) h += 1; /* may carry into exponent: correct */
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return sign;                              /* below half the smallest subnormal */
+    /* subnormal half: value = m * 2^-24 with m = round(|f| * 2^24) */
+    man |= 0x800000;                                       /* implicit one, value = man * 2^(e-23) */
+    const int shift = -e - 1;                              /* = (e-23) - (-24) negated: 14..24 */
+    const uint32_t m = man >> shift;
+    const uint32_t rem = man & ((1u << shift) - 1);
+    const uint32_t half = 1u << (shift - 1);
+    uint32_t h = m;
+    if (rem > half || (rem == half && (m & 1))) h += 1;
+    return (uint16_t)(sign | h);
+}
+
+void ora_fp16_to_fp32_n(const uint16_t *h, float *f, size_t n) {
+    for (size_t i = 0; i < n; ++i) f[i] = ora_fp16_to_fp32(h[i]);
+}
+void ora_fp32_to_fp16_n(const float *f, uint16_t *h, size_t n) {
+    for (size_t i = 0; i < n; ++i) h[i] = ora_fp32_to_fp16(f[i]);
+}
+
+/* ------------------------------------------------------------ dequant -- */
+
+/* 6-bit (scale, min) pair j in [0, 8) of the 12 packed bytes.
+ * exec:690-693, debug/official_dequant.c:38-45. */
+void ora_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* debug/official_dequant.c:47-65; exec:920-951 (k_q4k_mv), :1233-1254 (k_q4k_embed).
+ * y[64g+l] = (d*sc_2g)*(qs[32g+l]&15) - dmin*m_2g, y[64g+32+l] likewise with the high
+ * nibble and pair 2g+1.  d*sc and (d*sc)*q are exact in fp32, so one rounding. */
+void ora_dequant_row_q4_K(const void *blocks, float *y, int64_t k) {
+    const ora_block_q4_K *x = (const ora_block_q4_K *)blocks;
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = ora_fp16_to_fp32(x[i].d);
+        const float dmin = ora_fp16_to_fp32(x[i].dmin);
+        const uint8_t *q = x[i].qs;
+        for (int g = 0; g < 4; ++g) {
+            uint8_t sc, m;
+            ora_get_scale_min_k4(2 * g, x[i].scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            ora_get_scale_min_k4(2 * g + 1, x[i].scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] & 0x0f) - m1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(q[l] >> 4) - m2;
+            q += 32;
+        }
+    }
+}
+
+/* exec:1026-1048 (q6k_val); debug/verify/verify_q6k_wqkv.py:5-34.
+ * For half h, l in [0,32), r in [0,4): q_r = 6-bit value (low nibble of ql[64h+l] or
+ * ql[64h+32+l], high nibble for r>=2; two bits 2r of qh[32h+l]) - 32;
+ * y[128h+32r+l] = (d*sc[8h+l/16+2r])*q_r.  Product order kept for signed zeros. */
+void ora_dequant_row_q6_K(const void *blocks, float *y, int64_t k) {
+    const ora_block_q6_K *x = (const ora_block_q6_K *)blocks;
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = ora_fp16_to_fp32(x[i].d);
+        for (int h = 0; h < 2; ++h) {
+            const uint8_t *ql = x[i].ql + 64 * h;
+            const uint8_t *qh = x[i].qh + 32 * h;
+            const int8_t *sc = x[i].scales + 8 * h;
+            float *yh = y + 256 * i + 128 * h;
+            for (int l = 0; l < 32; ++l) {
+                const int q0 = ((ql[l] & 0x0f) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q1 = ((ql[l + 32] & 0x0f) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q2 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q3 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                const int is = l / 16;
+                yh[l + 0] = d * (float)sc[is + 0] * (float)q0;
+                yh[l + 32] = d * (float)sc[is + 2] * (float)q1;
+                yh[l + 64] = d * (float)sc[is + 4] * (float)q2;
+                yh[l + 96] = d * (float)sc[is + 6] * (float)q3;
+            }
+        }
+    }
+}
+
+/* exec:1076-1096 (k_q80_mv): y = d*q. */
+void ora_dequant_row_q8_0(const void *blocks, float *y, int64_t k) {
+    const ora_block_q8_0 *x = (const ora_block_q8_0 *)blocks;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = ora_fp16_to_fp32(x[i].d);
+        for (int l = 0; l < 32; ++l) y[32 * i + l] = d * (float)x[i].qs[l];
+    }
+}
+
+int ora_dequant_rows(int type, const void *w, int rb, int rc, float *y) {
+    const int be = ora_block_elems(type);
+    const size_t ts = ora_type_size(type);
+    if (!be || rb <= 0 || rc <= 0) return -1;
+    const int64_t k = (int64_t)rb * be;
+    for (int r = 0; r < rc; ++r) {
+        const uint8_t *row = (const uint8_t *)w + (size_t)r * rb * ts;
+        float *yr = y + (size_t)r * k;
+        switch (type) {
+            case ORA_Q4_K: ora_dequant_row_q4_K(row, yr, k); break;
+            case ORA_Q6_K: ora_dequant_row_q6_K(row, yr, k); break;
+            case ORA_Q8_0: ora_dequant_row_q8_0(row, yr, k); break;
+            case ORA_F16: ora_fp16_to_fp32_n((const uint16_t *)row, yr, (size_t)k); break;
+            case ORA_F32: memcpy(yr, row, (size_t)k * 4); break;
+            default: return -1;
+        }
+    }
+    return 0;
+}
+
+/* --------------------------------------------------------- quantizers -- */
+/* Block generators for synthetic weights.  Simple per-group min/max fits; they
+ * only need to produce valid, well-spread blocks (not ggml's search). */
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+void ora_quantize_row_q4_K(const float *x, void *blocks, int64_t k) {
+    ora_block_q4_K *y = (ora_block_q4_K *)blocks;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        float scale[8], mn[8], maxs = 0.f, maxm = 0.f;
+        for (int j = 0; j < 8; ++j) {
+            float lo = 0.f, hi = 0.f;  /* min clamped to <= 0 so the offset is a subtraction */
+            for (int l = 0; l < 32; ++l) {
+                const float v = x[32 * j + l];
+                if (v < lo) lo = v;
+                if (v > hi) hi = v;
+            }
+            scale[j] = (hi - lo) / 15.f;
+            mn[j] = -lo;
+            if (scale[j] > maxs) maxs = scale[j];
+            if (mn[j] > maxm) maxm = mn[j];
+        }
+        const uint16_t dh = ora_fp32_to_fp16(maxs / 63.f), mh = ora_fp32_to_fp16(maxm / 63.f);
+        const float d = ora_fp16_to_fp32(dh), dmin = ora_fp16_to_fp32(mh);
+        uint8_t sc[8], m[8];
+        for (int j = 0; j < 8; ++j) {
+            sc[j] = (uint8_t)(d > 0.f ? clampi((int)lrintf(scale[j] / d), 0, 63) : 0);
+            m[j] = (uint8_t)(dmin > 0.f ? clampi((int)lrintf(mn[j] / dmin), 0, 63) : 0);
+        }
+        y[i].d = dh;
+        y[i].dmin = mh;
+        for (int j = 0; j < 4; ++j) {   /* inverse of ora_get_scale_min_k4 */
+            y[i].scales[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            y[i].scales[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            y[i].scales[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t L[256];
+        for (int j = 0; j < 8; ++j) {
+            const float ds = d * (float)sc[j], dm = dmin * (float)m[j];
+            for (int l = 0; l < 32; ++l) {
+                const float v = x[32 * j + l];
+                L[32 * j + l] = (uint8_t)(ds > 0.f ? clampi((int)lrintf((v + dm) / ds), 0, 15) : 0);
+            }
+        }
+        for (int g = 0; g < 4; ++g)
+            for (int l = 0; l < 32; ++l)
+                y[i].qs[32 * g + l] = (uint8_t)(L[64 * g + l] | (L[64 * g + 32 + l] << 4));
+    }
+}
+
+void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k) {
+    ora_block_q6_K *y = (ora_block_q6_K *)blocks;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        float scale[16], maxa = 0.f;
+        for (int j = 0; j < 16; ++j) {   /* group j = values [16j, 16j+16) <-> scales[j] */
+            float amax = 0.f, vmax = 0.f;
+            for (int l = 0; l < 16; ++l) {
+                const float v = x[16 * j + l];
+                if (fabsf(v) > amax) { amax = fabsf(v); vmax = v; }
+            }
+            scale[j] = vmax / -32.f;       /* the extreme value maps to code -32 */
+            if (fabsf(scale[j]) > maxa) maxa = fabsf(scale[j]);
+        }
+        const uint16_t dh = ora_fp32_to_fp16(maxa / 127.f);
+        const float d = ora_fp16_to_fp32(dh);
+        int8_t sc[16];
+        uint8_t L[256];
+        for (int j = 0; j < 16; ++j) {
+            sc[j] = (int8_t)(d > 0.f ? clampi((int)lrintf(scale[j] / d), -128, 127) : 0);
+            const float ds = d * (float)sc[j];
+            for (int l = 0; l < 16; ++l) {
+                const int q = ds != 0.f ? clampi((int)lrintf(x[16 * j + l] / ds), -32, 31) : 0;
+                L[16 * j + l] = (uint8_t)(q + 32);
+            }
+        }
+        for (int h = 0; h < 2; ++h) {
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q0 = L[128 * h + l], q1 = L[128 * h + 32 + l];
+                const uint8_t q2 = L[128 * h + 64 + l], q3 = L[128 * h + 96 + l];
+                y[i].ql[64 * h + l] = (uint8_t)((q0 & 15) | ((q2 & 15) << 4));
+                y[i].ql[64 * h + 32 + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+                y[i].qh[32 * h + l] = (uint8_t)((q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6));
+            }
+        }
+        memcpy(y[i].scales, sc, 16);
+        y[i].d = dh;
+    }
+}
+
+void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k) {
+    ora_block_q8_0 *y = (ora_block_q8_0 *)blocks;
+    for (int64_t i = 0; i < k / 32; ++i, x += 32) {
+        float amax = 0.f;
+        for (int l = 0; l < 32; ++l) if (fabsf(x[l]) > amax) amax = fabsf(x[l]);
+        y[i].d = ora_fp32_to_fp16(amax / 127.f);
+        const float d = ora_fp16_to_fp32(y[i].d);
+        for (int l = 0; l < 32; ++l)
+            y[i].qs[l] = (int8_t)(d > 0.f ? clampi((int)lrintf(x[l] / d), -127, 127) : 0);
+    }
+}
+
+/* ------------------------------------------------ activation quantizer -- */
+
+/* One 32-value group.  The reference (exec:84-107) uses d = amax/127 and
+ * q = roundf(x/d) under fast-math with no clamp; this path fixes the rule as
+ * IEEE x/d, round half away from zero (roundf), clamp to +-127, fp32 d. */
+static void quant_group32(const float *x, int8_t *q, float *d, uint32_t *s) {
+    float amax = 0.f;
+    for (int l = 0; l < 32; ++l) {
+        const float a = fabsf(x[l]);
+        if (a > amax) amax = a;
+    }
+    const float dd = amax / 127.f;
+    int lo = 0, hi = 0;
+    for (int l = 0; l < 32; ++l) {
+        int v = 0;
+        if (amax != 0.f) v = clampi((int)roundf(x[l] / dd), -127, 127);
+        q[l] = (int8_t)v;
+        if (l < 16) lo += v; else hi += v;
+    }
+    *d = dd;
+    *s = (uint32_t)(uint16_t)(int16_t)lo | ((uint32_t)(uint16_t)(int16_t)hi << 16);
+}
+
+void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s) {
+    for (int64_t j = 0; j < k / 32; ++j) quant_group32(x + 32 * j, q + 32 * j, d + j, s + j);
+}
+
+void ora_quant_act_gated(const float *x, const float *g, int64_t k, int8_t *q, float *d, uint32_t *s) {
+    float t[32];
+    for (int64_t j = 0; j < k / 32; ++j) {
+        for (int l = 0; l < 32; ++l) {
+            const float sig = 1.0f / (1.0f + expf(-g[32 * j + l]));
+            t[l] = x[32 * j + l] * sig;
+        }
+        quant_group32(t, q + 32 * j, d + j, s + j);
+    }
+}
+
+static int s16lo(uint32_t s) { return (int)(int16_t)(s & 0xffff); }
+static int s16hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
+
+/* Integer dot of one row against the activation format.  Per weight type:
+ *  Q4_K (exec:250-310 semantics): per block b and 32-group j,
+ *      d*sc_j*dx_j*sum(q4*q8) - dmin*m_j*dx_j*sum(q8)
+ *  Q6_K (exec:586-628): per 16-group j, d*sc_j*dx_(j/2)*sum((q6-32)*q8)
+ *  Q8_0 (exec:535-580): per block b, d_w*dx_b*sum(q*q8)
+ * Integer partial sums are exact; the fp64 combine has relative error ~1e-16. */
+double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const float *d,
+                   const uint32_t *s, double *norm) {
+    double acc = 0.0, nrm = 0.0;
+    if (type == ORA_Q4_K) {
+        const ora_block_q4_K *w = (const ora_block_q4_K *)wrow;
+        for (int b = 0; b < rb; ++b) {
+            const double dw = ora_fp16_to_fp32(w[b].d), dm = ora_fp16_to_fp32(w[b].dmin);
+            for (int j = 0; j < 8; ++j) {
+                uint8_t sc, m;
+                ora_get_scale_min_k4(j, w[b].scales, &sc, &m);
+                const int g = j / 2, hi = j & 1;
+                int sumi = 0;
+                for (int l = 0; l < 32; ++l) {
+                    const int qw = hi ? (w[b].qs[32 * g + l] >> 4) : (w[b].qs[32 * g + l] & 15);
+                    sumi += qw * q[256 * b + 32 * j + l];
+                }
+                const int S = s16lo(s[8 * b + j]) + s16hi(s[8 * b + j]);
+                const double dx = d[8 * b + j];
+                const double t1 = dw * sc * dx * sumi, t2 = dm * m * dx * S;
+                acc += t1 - t2;
+                nrm += fabs(t1) + fabs(t2);
+            }
+        }
+    } else if (type == ORA_Q6_K) {
+        const ora_block_q6_K *w = (const ora_block_q6_K *)wrow;
+        for (int b = 0; b < rb; ++b) {
+            /* 6-bit codes decoded with the index map of ora_dequant_row_q6_K */
+            const double dw = ora_fp16_to_fp32(w[b].d);
+            int code[256];
+            for (int h = 0; h < 2; ++h)
+                for (int l = 0; l < 32; ++l) {
+                    const uint8_t a = w[b].ql[64 * h + l], c = w[b].ql[64 * h + 32 + l], e = w[b].qh[32 * h + l];
+                    code[128 * h + l] = ((a & 15) | (((e >> 0) & 3) << 4)) - 32;
+                    code[128 * h + 32 + l] = ((c & 15) | (((e >> 2) & 3) << 4)) - 32;
+                    code[128 * h + 64 + l] = ((a >> 4) | (((e >> 4) & 3) << 4)) - 32;
+                    code[128 * h + 96 + l] = ((c >> 4) | (((e >> 6) & 3) << 4)) - 32;
+                }
+            for (int j = 0; j < 16; ++j) {
+                int sumi = 0;
+                for (int l = 0; l < 16; ++l) sumi += code[16 * j + l] * q[256 * b + 16 * j + l];
+                const double t = dw * w[b].scales[j] * (double)d[8 * b + j / 2] * sumi;
+                acc += t;
+                nrm += fabs(t);
+            }
+        }
+    } else if (type == ORA_Q8_0) {
+        const ora_block_q8_0 *w = (const ora_block_q8_0 *)wrow;
+        for (int b = 0; b < rb; ++b) {
+            int sumi = 0;
+            for (int l = 0; l < 32; ++l) sumi += w[b].qs[l] * q[32 * b + l];
+            const double t = (double)ora_fp16_to_fp32(w[b].d) * (double)d[b] * sumi;
+            acc += t;
+            nrm += fabs(t);
+        }
+    } else {
+        return NAN;
+    }
+    if (norm) *norm = nrm;
+    return acc;
+}
+
+int ora_gemv_act(int type, const void *w, int rb, int rc, const int8_t *q, const float *d,
+                 const uint32_t *s, double *y, double *norm) {
+    const size_t ts = ora_type_size(type);
+    if (!ts || (type != ORA_Q4_K && type != ORA_Q6_K && type != ORA_Q8_0)) return -1;
+    for (int r = 0; r < rc; ++r)
+        y[r] = ora_dot_act(type, (const uint8_t *)w + (size_t)r * rb * ts, rb, q, d, s, norm ? norm + r : NULL);
+    return 0;
+}
+
+int ora_gemv_f64(int type, const void *w, int rb, int rc, const float *x, double *y) {
+    const int be = ora_block_elems(type);
+    if (!be) return -1;
+    const int64_t k = (int64_t)rb * be;
+    float *row = (float *)malloc((size_t)k * sizeof(float));
+    if (!row) return -1;
+    const size_t rs = (size_t)rb * ora_type_size(type);
+    for (int r = 0; r < rc; ++r) {
+        if (ora_dequant_rows(type, (const uint8_t *)w + (size_t)r * rs, rb, 1, row)) { free(row); return -1; }
+        double acc = 0.0;
+        for (int64_t i = 0; i < k; ++i) acc += (double)row[i] * (double)x[i];
+        y[r] = acc;
+    }
+    free(row);
+    return 0;
+}
+
+/* ------------------------- the reference's own dp4a formulations (q8_1) -- */
+
+static int dp4(int a, int b, int c) {
+    const int8_t *x = (const int8_t *)&a, *y = (const int8_t *)&b;
+    return c + x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+}
+
+/* exec:84-107 with IEEE division: d = amax/127, q = roundf(x/d), ds = (d, sum x). */
+void ora_quant_q8_1(const float *x, int64_t k, ora_block_q8_1 *y) {
+    for (int64_t i = 0; i < k / 32; ++i) {
+        float amax = 0.f, sum = 0.f;
+        for (int l = 0; l < 32; ++l) {
+            const float v = x[32 * i + l];
+            if (fabsf(v) > amax) amax = fabsf(v);
+            sum += v;
+        }
+        const float d = amax / 127.f;
+        for (int l = 0; l < 32; ++l) y[i].qs[l] = (int8_t)(amax == 0.f ? 0 : (int)roundf(x[32 * i + l] / d));
+        y[i].d = ora_fp32_to_fp16(d);
+        y[i].s = ora_fp32_to_fp16(sum);
+    }
+}
+
+static int load_i32(const void *p) { int v; memcpy(&v, p, 4); return v; }
+
+/* exec:250-310: one thread's share iqs in {0,2,..,30} of one block, summed. */
+float ora_ref_vec_dot_q4_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb) {
+    const ora_block_q4_K *w = (const ora_block_q4_K *)wrow;
+    float total = 0.f;
+    for (int kbx = 0; kbx < rb; ++kbx) {
+        const ora_block_q4_K *bq = w + kbx;
+        const ora_block_q8_1 *b8 = xq + 8 * kbx;
+        for (int iqs = 0; iqs < 32; iqs += 2) {
+            const int bq8_offset = 2 * ((iqs / 2) / 4);
+            const uint8_t *q4 = bq->qs + 16 * bq8_offset + 4 * ((iqs / 2) % 4);
+            const int v0 = load_i32(q4), v1 = load_i32(q4 + 16);
+            uint16_t sc16[6], aux[2];
+            memcpy(sc16, bq->scales, 12);
+            const int j = bq8_offset / 2;
+            if (j < 2) {
+                aux[0] = (uint16_t)(sc16[j + 0] & 0x3f3f);
+                aux[1] = (uint16_t)(sc16[j + 2] & 0x3f3f);
+            } else {
+                aux[0] = (uint16_t)(((sc16[j + 2] >> 0) & 0x0f0f) | ((sc16[j - 2] & 0xc0c0) >> 2));
+                aux[1] = (uint16_t)(((sc16[j + 2] >> 4) & 0x0f0f) | ((sc16[j - 0] & 0xc0c0) >> 2));
+            }
+            const uint8_t *sc = (const uint8_t *)aux, *m = sc + 2;
+            float sumf_d = 0.f, sumf_m = 0.f;
+            for (int i = 0; i < 2; ++i) {
+                const ora_block_q8_1 *b8i = b8 + bq8_offset + i;
+                const float d8 = ora_fp16_to_fp32(b8i->d);
+                const int u0 = load_i32(b8i->qs + 4 * ((iqs / 2) % 4));
+                const int u1 = load_i32(b8i->qs + 4 * ((iqs / 2) % 4) + 16);
+                const int v0i = (v0 >> (4 * i)) & 0x0f0f0f0f, v1i = (v1 >> (4 * i)) & 0x0f0f0f0f;
+                const int dot1 = dp4(v1i, u1, dp4(v0i, u0, 0));
+                const int dot2 = dp4(0x01010101, u1, dp4(0x01010101, u0, 0));
+                sumf_d += d8 * (float)(dot1 * sc[i]);
+                sumf_m += d8 * (float)(dot2 * m[i]);
+            }
+            total += ora_fp16_to_fp32(bq->d) * sumf_d - ora_fp16_to_fp32(bq->dmin) * sumf_m;
+        }
+    }
+    return total;
+}
+
+/* per-byte saturating signed subtract (the __vsubss4 of exec:596) */
+static int vsubss4(int a, int b) {
+    int8_t x[4], y[4], r[4];
+    memcpy(x, &a, 4); memcpy(y, &b, 4);
+    for (int i = 0; i < 4; ++i) {
+        int v = x[i] - y[i];
+        r[i] = (int8_t)(v < -128 ? -128 : (v > 127 ? 127 : v));
+    }
+    int o; memcpy(&o, r, 4);
+    return o;
+}
+
+/* exec:586-628: iqs in [0,32) per block. */
+float ora_ref_vec_dot_q6_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb) {
+    const ora_block_q6_K *w = (const ora_block_q6_K *)wrow;
+    float total = 0.f;
+    for (int kbx = 0; kbx < rb; ++kbx) {
+        const ora_block_q6_K *bq = w + kbx;
+        const ora_block_q8_1 *b8 = xq + 8 * kbx;
+        for (int iqs = 0; iqs < 32; ++iqs) {
+            const int bq8_offset = 4 * (iqs / 16) + (iqs % 16) / 8;
+            const int scale_offset = 8 * (iqs / 16) + (iqs % 16) / 4;
+            const int vh_shift = 2 * ((iqs % 16) / 8);
+            const int vl = load_i32(bq->ql + 4 * iqs);
+            const int vh = (int)((uint32_t)load_i32(bq->qh + 4 * (8 * (iqs / 16) + iqs % 8)) >> vh_shift);
+            const int8_t *scales = bq->scales + scale_offset;
+            float sumf = 0.f;
+            for (int i = 0; i < 2; ++i) {
+                const int u = load_i32(b8[bq8_offset + 2 * i].qs + 4 * (iqs % 8));
+                const float d8 = ora_fp16_to_fp32(b8[bq8_offset + 2 * i].d);
+                const int sc = scales[4 * i];
+                const int vil = (int)(((uint32_t)vl >> (4 * i)) & 0x0f0f0f0f);
+                const int vih = (int)((((uint32_t)vh >> (4 * i)) << 4) & 0x30303030);
+                const int vi = vsubss4(vil | vih, 0x20202020);
+                sumf += d8 * (float)(dp4(vi, u, 0) * sc);
+            }
+            total += ora_fp16_to_fp32(bq->d) * sumf;
+        }
+    }
+    return total;
+}
+
+/* exec:535-580 */
+float ora_ref_vec_dot_q8_0_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb) {
+    const ora_block_q8_0 *w = (const ora_block_q8_0 *)wrow;
+    float total = 0.f;
+    for (int b = 0; b < rb; ++b) {
+        int sumi = 0;
+        for (int i = 0; i < 8; ++i) sumi = dp4(load_i32(w[b].qs + 4 * i), load_i32(xq[b].qs + 4 * i), sumi);
+        total += ora_fp16_to_fp32(w[b].d) * ora_fp16_to_fp32(xq[b].d) * (float)sumi;
+    }
+    return total;
+}
+
+/* ------------------------------------ ggml CPU path (parity unpinned) -- */
+/* Restatement of ggml's generic C routines quantize_row_q8_K_ref,
+ * ggml_vec_dot_q4_K_q8_K, ggml_vec_dot_q6_K_q8_K, quantize_row_q8_0 and
+ * ggml_vec_dot_q8_0_q8_0 (the vendored ref/llama.cpp that BASELINE names is an
+ * empty directory in the reference; no version is pinned).  CPU baseline only. */
+
+static int nearest_int(float f) { return (int)lrintf(f); }  /* round half to even */
+
+void ora_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
+    ora_block_q8_K *y = (ora_block_q8_K *)vy;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        float amax = 0.f, vmax = 0.f;
+        for (int j = 0; j < 256; ++j)
+            if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); vmax = x[j]; }
+        memset(&y[i], 0, sizeof y[i]);
+        if (amax == 0.f) continue;
+        const float iscale = -127.f / vmax;
+        for (int j = 0; j < 256; ++j) {
+            const int v = nearest_int(iscale * x[j]);
+            y[i].qs[j] = (int8_t)(v > 127 ? 127 : v);
+        }
+        for (int j = 0; j < 16; ++j) {
+            int sum = 0;
+            for (int l = 0; l < 16; ++l) sum += y[i].qs[16 * j + l];
+            y[i].bsums[j] = (int16_t)sum;
+        }
+        y[i].d = 1.f / iscale;
+    }
+}
+
+float ora_vec_dot_q4_K_q8_K(int n, const void *vx, const void *vy) {
+    const ora_block_q4_K *x = (const ora_block_q4_K *)vx;
+    const ora_block_q8_K *y = (const ora_block_q8_K *)vy;
+    float sums[8] = {0}, sumf = 0.f;
+    for (int i = 0; i < n / 256; ++i) {
+        int8_t a[256];
+        for (int g = 0; g < 4; ++g)
+            for (int l = 0; l < 32; ++l) {
+                a[64 * g + l] = (int8_t)(x[i].qs[32 * g + l] & 15);
+                a[64 * g + 32 + l] = (int8_t)(x[i].qs[32 * g + l] >> 4);
+            }
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) ora_get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
+        int sumi = 0;
+        for (int j = 0; j < 16; ++j) sumi += y[i].bsums[j] * mn[j / 2];
+        int aux32[8] = {0};
+        for (int j = 0; j < 8; ++j)
+            for (int l = 0; l < 32; ++l) aux32[l % 8] += sc[j] * (a[32 * j + l] * y[i].qs[32 * j + l]);
+        const float d = ora_fp16_to_fp32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+        const float dmin = ora_fp16_to_fp32(x[i].dmin) * y[i].d;
+        sumf -= dmin * (float)sumi;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+float ora_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
+    const ora_block_q6_K *x = (const ora_block_q6_K *)vx;
+    const ora_block_q8_K *y = (const ora_block_q8_K *)vy;
+    float sums[8] = {0}, sumf = 0.f;
+    for (int i = 0; i < n / 256; ++i) {
+        int8_t a[256];
+        for (int h = 0; h < 2; ++h)
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t p = x[i].ql[64 * h + l], c = x[i].ql[64 * h + 32 + l], e = x[i].qh[32 * h + l];
+                a[128 * h + l] = (int8_t)(((p & 15) | (((e >> 0) & 3) << 4)) - 32);
+                a[128 * h + 32 + l] = (int8_t)(((c & 15) | (((e >> 2) & 3) << 4)) - 32);
+                a[128 * h + 64 + l] = (int8_t)(((p >> 4) | (((e >> 4) & 3) << 4)) - 32);
+                a[128 * h + 96 + l] = (int8_t)(((c >> 4) | (((e >> 6) & 3) << 4)) - 32);
+            }
+        int aux32[8] = {0};
+        for (int j = 0; j < 16; ++j)
+            for (int l = 0; l < 16; ++l) aux32[l % 8] += x[i].scales[j] * (a[16 * j + l] * y[i].qs[16 * j + l]);
+        const float d = ora_fp16_to_fp32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+void ora_quantize_row_q8_0_act(const float *x, void *vy, int64_t k) {
+    ora_block_q8_0 *y = (ora_block_q8_0 *)vy;
+    for (int64_t i = 0; i < k / 32; ++i, x += 32) {
+        float amax = 0.f;
+        for (int l = 0; l < 32; ++l) if (fabsf(x[l]) > amax) amax = fabsf(x[l]);
+        const float d = amax / 127.f, id = d != 0.f ? 1.f / d : 0.f;
+        y[i].d = ora_fp32_to_fp16(d);
+        for (int l = 0; l < 32; ++l) y[i].qs[l] = (int8_t)roundf(x[l] * id);
+    }
+}
+
+float ora_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy) {
+    const ora_block_q8_0 *x = (const ora_block_q8_0 *)vx, *y = (const ora_block_q8_0 *)vy;
+    float sumf = 0.f;
+    for (int i = 0; i < n / 32; ++i) {
+        int sumi = 0;
+        for (int l = 0; l < 32; ++l) sumi += x[i].qs[l] * y[i].qs[l];
+        sumf += (float)sumi * (ora_fp16_to_fp32(x[i].d) * ora_fp16_to_fp32(y[i].d));
+    }
+    return sumf;
+}
+
+typedef struct {
+    int type, rb, r0, r1;
+    const uint8_t *w;
+    const void *xq;
+    float *y;
+} cpu_job;
+
+static void *cpu_worker(void *p) {
+    const cpu_job *j = (const cpu_job *)p;
+    const size_t rs = (size_t)j->rb * ora_type_size(j->type);
+    const int n = j->rb * ora_block_elems(j->type);
+    for (int r = j->r0; r < j->r1; ++r) {
+        const uint8_t *row = j->w + (size_t)r * rs;
+        if (j->type == ORA_Q4_K) j->y[r] = ora_vec_dot_q4_K_q8_K(n, row, j->xq);
+        else if (j->type == ORA_Q6_K) j->y[r] = ora_vec_dot_q6_K_q8_K(n, row, j->xq);
+        else j->y[r] = ora_vec_dot_q8_0_q8_0(n, row, j->xq);
+    }
+    return NULL;
+}
+
+int ora_gemv_cpu(int type, const void *w, int rb, int rc, const void *xq, float *y, int nthreads) {
+    if (type != ORA_Q4_K && type != ORA_Q6_K && type != ORA_Q8_0) return -1;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    cpu_job jobs[256];
+    for (int t = 0; t < nthreads; ++t) {
+        jobs[t].type = type; jobs[t].rb = rb; jobs[t].w = (const uint8_t *)w; jobs[t].xq = xq; jobs[t].y = y;
+        jobs[t].r0 = (int)((int64_t)rc * t / nthreads);
+        jobs[t].r1 = (int)((int64_t)rc * (t + 1) / nthreads);
+    }
+    if (nthreads == 1) { cpu_worker(&jobs[0]); return 0; }
+    for (int t = 0; t < nthreads; ++t) pthread_create(&th[t], NULL, cpu_worker, &jobs[t]);
+    for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+    return 0;
+}
+
+/* ------------------------------------------------------------- top-k -- */
+/* Candidate order of the reference's sampler (src/mono27b_chat.cpp:221-227:
+ * logits[a] > logits[b]) made total: value descending, then index ascending;
+ * -0.0 == +0.0 as floats; NaN after every number. */
+typedef struct { float v; int32_t i; } vi_pair;
+
+static int cmp_vi(const void *pa, const void *pb) {
+    const vi_pair *a = (const vi_pair *)pa, *b = (const vi_pair *)pb;
+    const int na = isnan(a->v), nb = isnan(b->v);
+    if (na != nb) return na ? 1 : -1;
+    if (!na) {
+        if (a->v > b->v) return -1;
+        if (a->v < b->v) return 1;
+    }
+    return (a->i > b->i) - (a->i < b->i);
+}
+
+int ora_topk(const float *v, int n, int k, int32_t *idx, float *val) {
+    if (n <= 0 || k <= 0 || k > n) return -1;
+    vi_pair *p = (vi_pair *)malloc((size_t)n * sizeof *p);
+    if (!p) return -1;
+    for (int i = 0; i < n; ++i) { p[i].v = v[i]; p[i].i = i; }
+    qsort(p, (size_t)n, sizeof *p, cmp_vi);
+    for (int i = 0; i < k; ++i) { idx[i] = p[i].i; val[i] = p[i].v; }
+    free(p);
+    return 0;
+}

@@ -1,0 +1,123 @@
+/*
+ * m27q_oracle.h -- CPU oracle for the quantized linear-algebra path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product path (libm27q.so) never links, loads or calls anything here.
+ *
+ * It restates, in plain C99, the arithmetic of the reference's quant path
+ * (eramax/mono-qwen27 @ src/mono27b_executor.cu, "exec" below) and of the
+ * ggml CPU routines that path mirrors.  Every routine cites the reference
+ * file:line it follows.  The GGUF block byte layouts are fixed by the file
+ * format and are therefore identical to the reference's structs.
+ *
+ * Parity pins (what checks each function independently of its own formula):
+ *   ora_fp16_to_fp32      all 65536 inputs vs numpy float16->float32, and vs the
+ *                         conversion inside debug/official_dequant.c built from
+ *                         the reference's source (oracle/_ref).
+ *   ora_fp32_to_fp16      vs numpy float32->float16 (round-to-nearest-even).
+ *   ora_dequant_row_q4_K  reference known-answer bytes (debug/official_dequant.c:71-74
+ *                         -> debug/mono_give_current.debug.tsv:2), random blocks vs
+ *                         dequantize_row_q4_K compiled from debug/official_dequant.c,
+ *                         and the reference's second formulation (the dp4a vec-dot,
+ *                         ora_ref_vec_dot_q4_K_q8_1) with one-hot activations.
+ *   ora_dequant_row_q6_K  the reference's dp4a vec-dot formulation
+ *                         (ora_ref_vec_dot_q6_K_q8_1, exec:586-628) with one-hot
+ *                         activations, plus single-bit known answers.
+ *   ora_dequant_row_q8_0  the reference's dp4a formulation (exec:535-580).
+ *   ora_quant_act         closed-form properties (|q|<=127, the max maps to +-127,
+ *                         |x - d q| <= d/2, round-half-away on constructed ties).
+ *   ora_dot_act           brute force (dequantized weights x dequantized activation
+ *                         in fp64) on small shapes, and one-hot / zero inputs.
+ *   ora_topk              numpy lexsort on the same values.
+ *   ggml q8_K routines    PARITY UNPINNED: ggml itself (ref/llama.cpp) is absent from
+ *                         the reference checkout and no version is pinned.  They are a
+ *                         restatement of ggml's published generic C path, used only as
+ *                         the CPU baseline and as the "no worse than q8_K" yardstick.
+ *   quantizers            not parity functions: they only generate valid blocks.
+ */
+#ifndef M27Q_ORACLE_H
+#define M27Q_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (include/mono27b_gguf.h:27-43 in the reference). */
+enum { ORA_F32 = 0, ORA_F16 = 1, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q6_K = 14, ORA_Q8_K = 15 };
+
+/* GGUF block layouts (exec:18-23, :25-28, :38-42, :57-62). */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } ora_block_q4_K;
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } ora_block_q6_K;
+typedef struct { uint16_t d; int8_t qs[32]; } ora_block_q8_0;
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } ora_block_q8_K;
+/* The reference's activation block (exec:65-71): half2 {d, sum(x)} + 32 codes. */
+typedef struct { uint16_t d, s; int8_t qs[32]; } ora_block_q8_1;
+
+size_t ora_type_size(int type);   /* bytes per block (src/mono27b_gguf.cpp:167-180) */
+int    ora_block_elems(int type); /* weights per block (src/mono27b_gguf.cpp:182-195) */
+
+float    ora_fp16_to_fp32(uint16_t h);
+uint16_t ora_fp32_to_fp16(float f);
+void     ora_fp16_to_fp32_n(const uint16_t *h, float *f, size_t n);
+void     ora_fp32_to_fp16_n(const float *f, uint16_t *h, size_t n);
+
+void ora_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
+
+/* Dequantization of k = n_blocks * block_elems weights. */
+void ora_dequant_row_q4_K(const void *blocks, float *y, int64_t k);
+void ora_dequant_row_q6_K(const void *blocks, float *y, int64_t k);
+void ora_dequant_row_q8_0(const void *blocks, float *y, int64_t k);
+/* rc rows of rb blocks each, GGUF row-major; F16/F32 rows of rb elements. */
+int  ora_dequant_rows(int type, const void *w, int rb, int rc, float *y);
+
+/* Seeded block generators (own simple min/max quantizers). */
+void ora_quantize_row_q4_K(const float *x, void *blocks, int64_t k);
+void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k);
+void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k);
+
+/* Activation format of the MI355X path: per 32 values, int8 codes, an fp32
+ * scale d = amax/127 (IEEE divide), q = roundf(x/d) clamped to +-127, and the
+ * two 16-value integer code sums packed as (int16 lo) | (int16 hi) << 16. */
+void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s);
+/* Same on x * sigmoid(g) (exec:109-138); sigmoid as 1/(1+expf(-g)). */
+void ora_quant_act_gated(const float *x, const float *g, int64_t k, int8_t *q, float *d, uint32_t *s);
+
+/* Integer-dot of one weight row against the activation format, evaluated in
+ * fp64 from the exact integer partial sums.  *norm (may be NULL) receives
+ * sum |term| over the per-group terms: the scale of fp32 reassociation error. */
+double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const float *d,
+                   const uint32_t *s, double *norm);
+int    ora_gemv_act(int type, const void *w, int rb, int rc, const int8_t *q, const float *d,
+                    const uint32_t *s, double *y, double *norm);
+
+/* fp64 dequant-then-dot: y[r] = sum_k W[r][k] x[k]. */
+int ora_gemv_f64(int type, const void *w, int rb, int rc, const float *x, double *y);
+
+/* Restatements of the reference's own dp4a vec-dot formulations, used to
+ * cross-check the dequant restatements (two independent codings of one format). */
+void  ora_quant_q8_1(const float *x, int64_t k, ora_block_q8_1 *y);
+float ora_ref_vec_dot_q4_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
+float ora_ref_vec_dot_q6_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
+float ora_ref_vec_dot_q8_0_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
+
+/* ggml CPU path restatement (parity unpinned; CPU baseline). */
+void  ora_quantize_row_q8_K(const float *x, void *y, int64_t k);
+float ora_vec_dot_q4_K_q8_K(int n, const void *vx, const void *vy);
+float ora_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy);
+void  ora_quantize_row_q8_0_act(const float *x, void *y, int64_t k);
+float ora_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy);
+/* y[r] for r in [0, rc), rows split over nthreads pthreads.  xq is the
+ * activation quantized to q8_K (K-quants) or q8_0 (Q8_0). */
+int ora_gemv_cpu(int type, const void *w, int rb, int rc, const void *xq, float *y, int nthreads);
+
+/* Exact top-k by (value desc, index asc); NaN ranks after every number. */
+int ora_topk(const float *v, int n, int k, int32_t *idx, float *val);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,253 @@
+"""M = 1 products on the GPU vs the oracle.
+
+int8-activation path: against the oracle's integer-dot formula evaluated in
+fp64 (tolerance 1e-5 x the sum of |per-group terms|: fp32 reassociation only),
+and against the fp64 dequant-then-dot oracle, no worse than the ggml q8_K CPU
+path on the same inputs.  fp32-activation path: within 1e-3 relative of the
+fp64 dequant-then-dot oracle (it lands near 1e-6 of sum |w x|).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import act_host, int_dot_tol, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {  # (type, rows, K)
+    "q4k_small": ("Q4_K", 40, 512),
+    "q4k_ffn": ("Q4_K", 17408, 5120),
+    "q4k_o": ("Q4_K", 5120, 6144),
+    "q6k_down": ("Q6_K", 5120, 17408),
+    "q6k_small": ("Q6_K", 24, 768),
+    "q80_2048": ("Q8_0", 2048, 2048),
+    "q80_down": ("Q8_0", 2048, 6144),
+    "q80_ragged": ("Q8_0", 13, 160),
+}
+
+_cache = {}
+
+
+def weights(ora, type_name, rc, k, seed):
+    key = (type_name, rc, k, seed)
+    if key not in _cache:
+        t = getattr(ora, type_name)
+        _cache[key] = ora.synth_weights(t, rc, k, seed)
+    return _cache[key]
+
+
+def quantized_x(m27q, dev, k, seed):
+    x = np.random.default_rng(seed).standard_normal(k).astype(np.float32)
+    act = m27q.Act(1, k, dev)
+    m27q.quant_act(to_dev(x, dev), act)
+    return x, act
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+@pytest.mark.parametrize("layout", [0, 1])
+def test_matvec_q8_vs_int_oracle(m27q, ora, dev, shape, layout):
+    import torch
+    type_name, rc, k = SHAPES[shape]
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, layout, dev)
+    x, act = quantized_x(m27q, dev, k, 1)
+    q, d, s = act_host(m27q, act)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("matvec_q8", shape, "layout", layout)
+    m27q.matvec_q8(w, act, y)
+    got = to_host(y).astype(np.float64)
+    want, nrm = ora.gemv_act(t, wb, rb, rc, q[0], d[0], s[0])
+    bad = np.abs(got - want) > int_dot_tol(nrm)
+    assert not bad.any(), (np.flatnonzero(bad)[:5], got[bad][:5], want[bad][:5])
+
+
+@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 17408, 5120), ("Q6_K", 5120, 17408), ("Q8_0", 6144, 2048)])
+def test_q8_path_no_worse_than_q8K_cpu_path(m27q, ora, dev, type_name, rc, k):
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    x, act = quantized_x(m27q, dev, k, 1)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("no-worse-than-q8K", type_name)
+    m27q.matvec_q8(w, act, y)
+    got = to_host(y).astype(np.float64)
+    exact = ora.gemv_f64(t, wb, rb, rc, x)
+    cpu = ora.gemv_cpu(t, wb, rb, rc, ora.quant_cpu_act(t, x), nthreads=8).astype(np.float64)
+    e_gpu = np.sqrt(np.mean((got - exact) ** 2))
+    e_cpu = np.sqrt(np.mean((cpu - exact) ** 2))
+    print(f"rms err gpu(per-32 int8)={e_gpu:.3e} cpu(q8_K/q8_0)={e_cpu:.3e} ratio={e_gpu / e_cpu:.3f}")
+    assert e_gpu <= e_cpu * 1.05
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_layouts_agree_and_residual(m27q, ora, dev, layout):
+    import torch
+    rc, k = 6144, 5120
+    wb = weights(ora, "Q4_K", rc, k, 12)
+    w = m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 20, rc, layout, dev)
+    x, act = quantized_x(m27q, dev, k, 2)
+    res = torch.from_numpy(np.random.default_rng(3).standard_normal(rc).astype(np.float32)).to(dev)
+    y0 = torch.empty(rc, dtype=torch.float32, device=dev)
+    y1 = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("residual", layout)
+    m27q.matvec_q8(w, act, y0)
+    m27q.matvec_q8(w, act, y1, residual=res)
+    a, b, r = to_host(y0), to_host(y1), to_host(res)
+    assert np.array_equal((a + r).view(np.uint32), b.view(np.uint32))
+
+
+def test_fused_output_quant_matches_standalone(m27q, ora, dev):
+    import torch
+    rc, k = 5120, 6144
+    wb = weights(ora, "Q4_K", rc, k, 13)
+    w = m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 24, rc, m27q.TILED, dev)
+    x, act = quantized_x(m27q, dev, k, 4)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    yq = m27q.Act(1, rc, dev)
+    say("fused output quant")
+    m27q.matvec_q8(w, act, y, yq=yq)
+    ref = m27q.Act(1, rc, dev)
+    m27q.quant_act(y, ref)
+    for a, b in zip(act_host(m27q, yq), act_host(m27q, ref)):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    qo, do, so = ora.quant_act(to_host(y))
+    assert np.array_equal(act_host(m27q, yq)[0][0], qo)
+
+
+def test_multi_matches_single(m27q, ora, dev):
+    import torch
+    k = 5120
+    shapes = [6144, 1024, 1024]
+    ws, wbs = [], []
+    for i, rc in enumerate(shapes):
+        wb = weights(ora, "Q4_K", rc, k, 20 + i)
+        wbs.append(wb)
+        ws.append(m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev))
+    x, act = quantized_x(m27q, dev, k, 5)
+    ys = [torch.empty(rc, dtype=torch.float32, device=dev) for rc in shapes]
+    say("multi q/k/v")
+    m27q.matvec_q8_multi(ws, act, ys)
+    q, d, s = act_host(m27q, act)
+    for wb, rc, y in zip(wbs, shapes, ys):
+        want, nrm = ora.gemv_act(m27q.Q4_K, wb, 20, rc, q[0], d[0], s[0])
+        assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+def test_ffn_swiglu(m27q, ora, dev, type_name):
+    import torch
+    t = getattr(m27q, type_name)
+    rc, k = 17408, 5120
+    gb = weights(ora, type_name, rc, k, 30)
+    ub = weights(ora, type_name, rc, k, 31)
+    gw = m27q.Weight.upload(gb.reshape(-1), t, 20, rc, m27q.TILED, dev)
+    uw = m27q.Weight.upload(ub.reshape(-1), t, 20, rc, m27q.TILED, dev)
+    x, act = quantized_x(m27q, dev, k, 6)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    yq = m27q.Act(1, rc, dev)
+    g = torch.empty(rc, dtype=torch.float32, device=dev)
+    u = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("swiglu", type_name)
+    m27q.ffn_swiglu(gw, uw, act, y, yq=yq)
+    m27q.matvec_q8(gw, act, g)
+    m27q.matvec_q8(uw, act, u)
+    gh, uh, yh = to_host(g).astype(np.float64), to_host(u).astype(np.float64), to_host(y).astype(np.float64)
+    silu = gh / (1 + np.exp(-gh))
+    assert np.allclose(yh, silu * uh, rtol=2e-6, atol=1e-7 * np.abs(silu * uh).max())
+    q, d, s = act_host(m27q, act)
+    want_g, ng = ora.gemv_act(t, gb, 20, rc, q[0], d[0], s[0])
+    assert (np.abs(gh - want_g) <= int_dot_tol(ng)).all()
+    ref = m27q.Act(1, rc, dev)
+    m27q.quant_act(y, ref)
+    for a, b in zip(act_host(m27q, yq), act_host(m27q, ref)):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+@pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged"])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_matvec_f32_vs_fp64(m27q, ora, dev, shape, layout):
+    import torch
+    type_name, rc, k = SHAPES[shape]
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, layout, dev)
+    x = np.random.default_rng(8).standard_normal(k).astype(np.float32)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("matvec_f32", shape, layout)
+    m27q.matvec_f32(w, to_dev(x, dev), y)
+    got = to_host(y).astype(np.float64)
+    want = ora.gemv_f64(t, wb, rb, rc, x)
+    scale = np.abs(ora.dequant(t, wb, rb, rc)).astype(np.float64) @ np.abs(x).astype(np.float64)
+    assert (np.abs(got - want) <= 1e-5 * scale).all()
+    rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-3 * scale)
+    assert rel.max() <= 1e-3
+
+
+@pytest.mark.parametrize("type_name", ["F16", "F32"])
+def test_matvec_dense(m27q, ora, dev, type_name):
+    import torch
+    t = getattr(m27q, type_name)
+    rc, k = 48, 5120
+    w32 = np.random.default_rng(2).standard_normal((rc, k)).astype(np.float32)
+    raw = ora.quantize(t, w32)
+    w = m27q.Weight.upload(raw.reshape(-1), t, k, rc, m27q.GGUF, dev)
+    x = np.random.default_rng(9).standard_normal(k).astype(np.float32)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("matvec dense", type_name)
+    m27q.matvec_f32(w, to_dev(x, dev), y)
+    want = ora.gemv_f64(t, raw, k, rc, x)
+    scale = np.abs(ora.dequant(t, raw, k, rc)).astype(np.float64) @ np.abs(x)
+    assert (np.abs(to_host(y) - want) <= 1e-5 * scale).all()
+
+
+def test_matvec_with_scratch_equals_two_step(m27q, ora, dev):
+    import torch
+    rc, k = 5120, 17408
+    wb = weights(ora, "Q6_K", rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), m27q.Q6_K, 68, rc, m27q.TILED, dev)
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    xd = to_dev(x, dev)
+    scratch = torch.empty(m27q.act_bytes(1, k), dtype=torch.uint8, device=dev)
+    y0 = torch.empty(rc, dtype=torch.float32, device=dev)
+    y1 = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("matvec with scratch")
+    m27q.matvec(w, xd, y0, scratch)
+    act = m27q.Act(1, k, dev)
+    m27q.quant_act(xd, act)
+    m27q.matvec_q8(w, act, y1)
+    assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 17408, 5120), ("Q6_K", 5120, 17408)])
+def test_properties_full_size(m27q, ora, dev, type_name, rc, k):
+    """Zero input -> exact zeros; x = 127 e_j -> 127 x column j of the dequantized matrix."""
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // 256
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    act = m27q.Act(1, k, dev)
+    say("zero input", type_name)
+    m27q.quant_act(torch.zeros(k, dtype=torch.float32, device=dev), act)
+    m27q.matvec_q8(w, act, y)
+    assert (to_host(y) == 0).all()
+    deq = torch.empty((rc, 256), dtype=torch.float32, device=dev)
+    for j in (0, 37, k // 2 + 131, k - 1):
+        x = torch.zeros(k, dtype=torch.float32, device=dev)
+        x[j] = 127.0
+        say("one-hot", type_name, j)
+        m27q.quant_act(x, act)
+        m27q.matvec_q8(w, act, y)
+        blk = j // 256
+        # column j of the dequantized matrix, via the GPU dequant (bit-exact, tested separately)
+        wcol = m27q.Weight.upload(np.ascontiguousarray(wb.reshape(rc, rb, -1)[:, blk]).reshape(-1), t, 1, rc,
+                                  m27q.GGUF, dev)
+        m27q.dequant_rows(wcol, 0, rc, deq)
+        col = to_host(deq)[:, j % 256].astype(np.float64)
+        got = to_host(y).astype(np.float64)
+        assert np.allclose(got, 127.0 * col, rtol=1e-6, atol=1e-6 * np.abs(127.0 * col).max())

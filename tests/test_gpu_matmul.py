@@ -1,0 +1,42 @@
+"""Small-M products (speculative-verify / prefill rows) vs M independent rows."""
+import numpy as np
+import pytest
+
+from gpu_util import act_host, int_dot_tol, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+_cache = {}
+
+CASES = [  # type, rows, K, M, layout
+    ("Q4_K", 6144, 5120, 1, 1), ("Q4_K", 6144, 5120, 2, 1), ("Q4_K", 6144, 5120, 4, 1),
+    ("Q4_K", 6144, 5120, 8, 1), ("Q4_K", 6144, 5120, 16, 1), ("Q4_K", 6144, 5120, 23, 0),
+    ("Q4_K", 40, 512, 5, 0), ("Q4_K", 40, 512, 64, 1),
+    ("Q6_K", 5120, 17408, 16, 1), ("Q6_K", 5120, 17408, 3, 0), ("Q6_K", 24, 768, 9, 1),
+    ("Q8_0", 2048, 6144, 16, 1), ("Q8_0", 2048, 6144, 2, 0), ("Q8_0", 13, 160, 7, 1),
+]
+
+
+@pytest.mark.parametrize("type_name,rc,k,M,layout", CASES)
+def test_matmul_vs_oracle(m27q, ora, dev, type_name, rc, k, M, layout):
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    key = (type_name, rc, k)
+    if key not in _cache:
+        _cache[key] = ora.synth_weights(t, rc, k, seed=40)
+    wb = _cache[key]
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, layout, dev)
+    X = np.random.default_rng(M).standard_normal((M, k)).astype(np.float32)
+    act = m27q.Act(M, k, dev)
+    m27q.quant_act(to_dev(X, dev), act)
+    res = np.random.default_rng(M + 1).standard_normal((M, rc)).astype(np.float32)
+    Y = torch.empty((M, rc), dtype=torch.float32, device=dev)
+    say("matmul", type_name, rc, k, M, layout)
+    m27q.matmul_q8(w, act, Y, residual=to_dev(res, dev))
+    got = to_host(Y).astype(np.float64) - res
+    q, d, s = act_host(m27q, act)
+    rows = range(M) if M <= 8 else [0, 1, M // 2, M - 2, M - 1]
+    for m in rows:
+        want, nrm = ora.gemv_act(t, wb, rb, rc, q[m], d[m], s[m])
+        assert (np.abs(got[m] - want) <= int_dot_tol(nrm) + 1e-6 * np.abs(res[m])).all(), m

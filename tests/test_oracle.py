@@ -1,0 +1,198 @@
+"""Pins the CPU oracle against checks independent of its own formulas.
+
+- fp16 conversion: numpy's float16 implementation, all 65536 inputs.
+- Q4_K dequant: the reference's known-answer block (official_dequant.c bytes ->
+  the values the reference's GPU embed wrote), and dequantize_row_q4_K compiled
+  from the reference's debug/official_dequant.c (oracle/_ref) on random blocks.
+- Q4_K / Q6_K / Q8_0 dequant: the reference's *other* formulation of each
+  format, its dp4a vec-dot (exec:250-310, :586-628, :535-580), driven with a
+  one-hot activation so that it returns one dequantized weight per position.
+- int-dot oracle: numpy fp64 matmul of dequantized weights and activations.
+- activation quantizer: closed-form properties and constructed ties.
+- top-k: numpy lexsort.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+RNG = np.random.default_rng(1234)
+
+
+def random_blocks(ora, type_, nblocks, rng=RNG):
+    """Random block bytes with finite fp16 scales (subnormals and negatives allowed)."""
+    ts = ora.TYPE_SIZE[type_]
+    b = rng.integers(0, 256, size=(nblocks, ts), dtype=np.uint8)
+    f16 = lambda n: (rng.standard_normal(n) * 0.05).astype(np.float16).view(np.uint16)
+    if type_ == ora.Q4_K:
+        b[:, 0:2] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
+        b[:, 2:4] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif type_ == ora.Q6_K:
+        b[:, 208:210] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif type_ == ora.Q8_0:
+        b[:, 0:2] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
+    # a few subnormal / zero scales
+    sub = np.array([0x0001, 0x03ff, 0x8001, 0x0000, 0x8000], np.uint16).view(np.uint8).reshape(5, 2)
+    for i in range(min(5, nblocks)):
+        off = {ora.Q4_K: 0, ora.Q6_K: 208, ora.Q8_0: 0}[type_]
+        b[i, off:off + 2] = sub[i]
+    return b
+
+
+def test_fp16_to_fp32_all_inputs(ora):
+    h = np.arange(65536, dtype=np.uint16)
+    got = ora.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert np.isnan(got[~fin]).all()
+
+
+def test_fp32_to_fp16_rne(ora):
+    f = (RNG.standard_normal(200000) * 10.0 ** RNG.integers(-9, 6, 200000)).astype(np.float32)
+    edge = np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8, 1e-9,
+                     np.inf, -np.inf], np.float32)
+    f = np.concatenate([f, edge])
+    with np.errstate(over="ignore"):
+        want = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ora.fp32_to_fp16(f), want)
+
+
+def test_q4k_known_answer_from_reference(ora):
+    kat = json.load(open(os.path.join(GOLDEN, "q4k_kat.json")))
+    block = np.zeros(144, np.uint8)
+    prefix = np.frombuffer(bytes.fromhex(kat["block_prefix_hex"]), np.uint8)
+    block[:32] = prefix
+    y = ora.dequant(ora.Q4_K, block, 1, 1)[0]
+    want = np.array(kat["expected_first16"], np.float32)
+    assert np.array_equal(y[:16].view(np.uint32), want.view(np.uint32))
+
+
+def test_q4k_matches_reference_c_build(ora):
+    ref = ora.ref_lib()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (needs the reference checkout at build time)")
+    blocks = random_blocks(ora, ora.Q4_K, 512)
+    got = ora.dequant(ora.Q4_K, blocks, 512, 1)[0]
+    want = np.empty(512 * 256, np.float32)
+    ref.dequantize_row_q4_K(blocks.ctypes.data, want.ctypes.data, 512 * 256)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K", "Q8_0"])
+def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
+    """x = 127 e_j quantizes to d = 1, code 127 at j: the reference's dp4a dot then
+    returns 127 * W[j] (rounded once or twice), which pins every position's
+    nibble/bit/scale index of the dequant restatement."""
+    t = getattr(ora, type_name)
+    be = ora.BLOCK_ELEMS[t]
+    rb = 2 if t != ora.Q8_0 else 8
+    k = rb * be
+    for trial in range(3):
+        blocks = random_blocks(ora, t, rb, np.random.default_rng(trial))
+        deq = ora.dequant(t, blocks, rb, 1)[0].astype(np.float64)
+        for j in range(k):
+            x = np.zeros(k, np.float32)
+            x[j] = 127.0
+            xq = ora.quant_q8_1(x)
+            v = ora.ref_vec_dot_q8_1(t, blocks.reshape(-1), xq, rb)
+            assert abs(v - 127.0 * deq[j]) <= 4e-7 * abs(127.0 * deq[j]) + 1e-30, (type_name, trial, j)
+
+
+def test_q6k_single_bit_layout(ora):
+    """Hand-set bits land where the ggml Q6_K layout puts them."""
+    blk = np.zeros(210, np.uint8)
+    blk[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)  # d = 1.0
+    blk[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)  # scales 1..16
+    blk[0] = 0x0F        # ql[0] low nibble -> q0 at position 0
+    blk[32 + 5] = 0xF0   # ql[37] high nibble -> q3 at position 96 + 5
+    blk[128 + 40] = 0xC0  # qh[40]: bits 6-7 -> q3 of half 1, l = 8 -> position 128 + 96 + 8
+    y = ora.dequant(ora.Q6_K, blk, 1, 1)[0]
+    want = np.full(256, -32.0, np.float32) * np.repeat(np.arange(1, 17, dtype=np.float32), 16)
+    want[0] = 1.0 * (15 - 32)
+    want[96 + 5] = 7.0 * (15 - 32)
+    want[128 + 96 + 8] = 15.0 * (48 - 32)
+    assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K", "Q8_0"])
+def test_int_dot_oracle_vs_numpy_bruteforce(ora, type_name):
+    t = getattr(ora, type_name)
+    be = ora.BLOCK_ELEMS[t]
+    rb, rc = (3, 16) if t != ora.Q8_0 else (24, 16)
+    k = rb * be
+    w = ora.synth_weights(t, rc, k, seed=5)
+    x = RNG.standard_normal(k).astype(np.float32)
+    q, d, s = ora.quant_act(x)
+    y, nrm = ora.gemv_act(t, w, rb, rc, q, d, s)
+    wd = ora.dequant(t, w, rb, rc).astype(np.float64)
+    xd = q.astype(np.float64) * np.repeat(d.astype(np.float64), 32)
+    want = wd @ xd
+    assert np.allclose(y, want, rtol=0, atol=1e-12 * np.abs(wd).sum(1).max() * np.abs(xd).max())
+    assert (nrm >= np.abs(y) * (1 - 1e-12)).all()
+
+
+def test_int_dot_oracle_special_cases(ora):
+    w = ora.synth_weights(ora.Q4_K, 8, 512, seed=9)
+    q, d, s = ora.quant_act(np.zeros(512, np.float32))
+    y, _ = ora.gemv_act(ora.Q4_K, w, 2, 8, q, d, s)
+    assert np.array_equal(y, np.zeros(8))
+    assert (q == 0).all() and (d == 0).all() and (s == 0).all()
+
+
+def test_quant_act_properties(ora):
+    x = (RNG.standard_normal((4, 1024)) * 10.0 ** RNG.integers(-6, 6, (4, 1))).astype(np.float32)
+    q, d, s = ora.quant_act(x)
+    g = x.reshape(4, -1, 32)
+    qg = q.reshape(4, -1, 32).astype(np.int64)
+    amax = np.abs(g).max(-1)
+    assert np.array_equal(d, (amax / np.float32(127)).astype(np.float32))
+    assert (np.abs(qg) <= 127).all()
+    assert (np.abs(qg).max(-1) == 127).all()
+    err = np.abs(g.astype(np.float64) - qg * d[..., None].astype(np.float64))
+    assert (err <= 0.5 * d[..., None] * (1 + 1e-6)).all()
+    lo = qg[..., :16].sum(-1)
+    hi = qg[..., 16:].sum(-1)
+    s = s.astype(np.int64)
+    assert np.array_equal(((s & 0xFFFF) ^ 0x8000) - 0x8000, lo)
+    assert np.array_equal(((s >> 16) ^ 0x8000) - 0x8000, hi)
+
+
+def test_quant_act_rounds_half_away_from_zero(ora):
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0  # d = 1 exactly
+    x[1:7] = [2.5, -2.5, 0.5, -0.5, 1.5, 126.5]
+    q, d, _ = ora.quant_act(x)
+    assert d[0] == 1.0
+    assert list(q[1:7]) == [3, -3, 1, -1, 2, 127]
+
+
+def test_topk_matches_lexsort(ora):
+    v = np.round(RNG.standard_normal(5000) * 4).astype(np.float32)  # many ties
+    v[10], v[20], v[30] = -0.0, 0.0, np.nan
+    v[40], v[50] = np.inf, -np.inf
+    idx, val = ora.topk(v, 64)
+    key = np.where(np.isnan(v), -np.inf, v)
+    nan_last = np.isnan(v).astype(np.int8)
+    order = np.lexsort((np.arange(v.size), -key, nan_last))
+    assert np.array_equal(idx, order[:64])
+    assert np.array_equal(val.view(np.uint32), v[order[:64]].view(np.uint32))
+    # -0.0 and +0.0 compare equal: index order decides
+    z = np.array([0.0, -0.0, 0.0, -0.0], np.float32)
+    assert list(ora.topk(z, 4)[0]) == [0, 1, 2, 3]
+
+
+def test_q8k_cpu_path_is_a_sane_approximation(ora):
+    """The ggml-semantics CPU path (parity unpinned) stays within its quantization error."""
+    for t in (ora.Q4_K, ora.Q6_K, ora.Q8_0):
+        k = 1024
+        w = ora.synth_weights(t, 32, k, seed=3)
+        x = RNG.standard_normal(k).astype(np.float32)
+        rb = k // ora.BLOCK_ELEMS[t]
+        y = ora.gemv_cpu(t, w, rb, 32, ora.quant_cpu_act(t, x), nthreads=2)
+        ref = ora.gemv_f64(t, w, rb, 32, x)
+        scale = np.abs(ora.dequant(t, w, rb, 32)).sum(1) * np.abs(x).max()
+        assert (np.abs(y - ref) <= 0.02 * scale).all()
