@@ -67,25 +67,48 @@ class Buffers:
     def __init__(self, m27q, dev):
         import torch
         self.x = torch.from_numpy(np.random.default_rng(1).standard_normal(5120).astype(np.float32)).to(dev)
-        self.xq = m27q.Act(1, 5120, dev)
         self.q = torch.empty(6144, dtype=torch.float32, device=dev)
         self.k = torch.empty(1024, dtype=torch.float32, device=dev)
         self.v = torch.empty(1024, dtype=torch.float32, device=dev)
-        self.qq = m27q.Act(1, 6144, dev)
         self.h = torch.empty(5120, dtype=torch.float32, device=dev)
-        self.hq = m27q.Act(1, 5120, dev)
         self.f = torch.empty(17408, dtype=torch.float32, device=dev)
         self.fq = m27q.Act(1, 17408, dev)
         self.out = torch.empty(5120, dtype=torch.float32, device=dev)
 
 
+# The layer's products in dependency order.  fp32 activations are quantized
+# inside each product; the SwiGLU product hands its output to down already
+# quantized.  o consumes the 6144-vector q in place of the attention output.
+STAGES = {
+    "qkv": lambda m27q, L, B, s: m27q.matvec_multi([L["q"], L["k"], L["v"]], B.x, [B.q, B.k, B.v], stream=s),
+    "o": lambda m27q, L, B, s: m27q.matvec(L["o"], B.q, B.h, residual=B.x, stream=s),
+    "gate_up": lambda m27q, L, B, s: m27q.ffn_swiglu(L["gate"], L["up"], B.h, B.f, yq=B.fq, stream=s),
+    "down": lambda m27q, L, B, s: m27q.matvec_q8(L["down"], B.fq, B.out, residual=B.h, stream=s),
+}
+STAGE_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
+
+
+def stage_bytes(m27q, name):
+    """Algorithmic HBM bytes of one product: GGUF weight bytes (unpadded) + fp32
+    activation in + fp32 output (+ residual read, + quantized output)."""
+    w = {n: (m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256, rc, k) for n, t, rc, k in LAYER}
+    wb = sum(w[n][0] for n in STAGE_WEIGHTS[name])
+    k = w[STAGE_WEIGHTS[name][0]][2]
+    rows = sum(w[n][1] for n in STAGE_WEIGHTS[name])
+    if name == "qkv":
+        return wb + 4 * k + 4 * rows
+    if name == "o":
+        return wb + 4 * k + 4 * rows + 4 * rows          # + residual
+    if name == "gate_up":
+        n = w["gate"][1]
+        return wb + 4 * k + 4 * n + (n + 8 * (n // 32))  # + quantized output
+    n = w["down"][1]
+    return wb + (k + 8 * (k // 32)) + 4 * n + 4 * n      # quantized input, + residual
+
+
 def layer_pass(m27q, L, B, stream):
-    m27q.quant_act(B.x, B.xq, stream=stream)
-    m27q.matvec_q8_multi([L["q"], L["k"], L["v"]], B.xq, [B.q, B.k, B.v], stream=stream)
-    m27q.quant_act(B.q, B.qq, stream=stream)  # stands in for attention: o consumes a 6144-vector
-    m27q.matvec_q8(L["o"], B.qq, B.h, yq=B.hq, stream=stream)
-    m27q.ffn_swiglu(L["gate"], L["up"], B.hq, B.f, yq=B.fq, stream=stream)
-    m27q.matvec_q8(L["down"], B.fq, B.out, stream=stream)
+    for fn in STAGES.values():
+        fn(m27q, L, B, stream)
 
 
 def capture(torch, fn):
@@ -180,15 +203,17 @@ def main():
     ms_cold = time_graph(torch, g_cold, reps) / copies
     ms_warm = time_graph(torch, g_warm, reps) / copies
 
-    # Dominant kernel: the fused gate/up Q4_K SwiGLU product (100 MB of the layer's 215 MB).
-    def swiglu_pass(s):
-        for L in layers:
-            m27q.ffn_swiglu(L["gate"], L["up"], B.hq, B.f, yq=B.fq, stream=s)
-    g_sw = capture(torch, swiglu_pass)
-    g_sw.replay()
-    sw_ms = time_graph(torch, g_sw, max(1, reps)) / copies
-    sw_bytes = 2 * 50135040 + m27q.act_bytes(1, 5120) + 17408 * 4 + m27q.act_bytes(1, 17408)
-    sw_gbs = sw_bytes / (sw_ms * 1e-3) / 1e9
+    # Each product on its own, over the same rotated copies: average launch
+    # duration from HIP events on the replay stream.
+    stages = {}
+    for name, fn in STAGES.items():
+        g = capture(torch, lambda st, fn=fn: [fn(m27q, L, B, st) for L in layers])
+        g.replay()
+        ms = time_graph(torch, g, reps) / copies
+        nbytes = stage_bytes(m27q, name)
+        stages[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        log(f"{name}: {ms * 1e3:.2f} us, {stages[name]['GBps']} GB/s")
+    dom = stages["gate_up"]  # the dominant product: 100 MB of the layer's 215 MB
 
     gbs = layer_bytes / (ms_cold * 1e-3) / 1e9
     rec = {
@@ -205,10 +230,12 @@ def main():
         "lower_bound_us": round(layer_bytes / HBM_PEAK_GBS / 1e3, 2),
         "x_lower_bound": round(ms_cold * 1e3 / (layer_bytes / HBM_PEAK_GBS / 1e3), 3),
         "warm_us_per_layer": round(ms_warm * 1e3, 2),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_q8<Q4K,TILED,swiglu> (gate+up 17408x5120)",
-                     "achieved": round(sw_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(sw_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(sw_ms * 1e3, 3), "algorithmic_bytes": sw_bytes},
+        "stages": stages,
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_q8<Q4K,TILED,SWIGLU> (gate+up 17408x5120, fp32 x in, "
+                                               "fp32 + quantized out)",
+                     "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": dom["us"], "algorithmic_bytes": dom["bytes"]},
     }
     if not args.no_cpu:
         log("cpu baseline")

@@ -125,31 +125,50 @@ M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int
                                           hipStream_t stream);
 
 /* ------------------------------------------------------------------------
- * M = 1 matrix-vector products
+ * M = 1 matrix-vector products (integer dot: int8 activation codes x weight
+ * codes, fp32 combine).  Q4_K, Q6_K, Q8_0 weights in either layout.
+ *
+ * The activation is given either as fp32 values x[K] (16-byte aligned),
+ * quantized inside the product with exactly the rule of m27q_quant_act (the
+ * codes are identical),
+ * or as an already quantized buffer xq from m27q_quant_act (M = 1, K = the
+ * weight's K).  Where yq is not NULL, the output y is also quantized into yq
+ * (the format of m27q_quant_act with K = row_count, which must be a multiple
+ * of 32): the fused producer of the next product's activation.
  * ---------------------------------------------------------------------- */
 
-/* y[r] = sum_k W[r][k] * xq[k] (+ residual[r]) on an already-quantized
- * activation (m27q_quant_act with M = 1 and K = the weight's K).  Q4_K, Q6_K,
- * Q8_0.  residual may be NULL.  If yq is not NULL, y is also quantized into yq
- * (format of m27q_quant_act, K = row_count, which must be a multiple of 32):
- * the fused producer of the next projection's activation.
- * Replaces l_mv_q8_on (exec:2054-2083) and k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a
- * / k_q80_mv_q8_dp4a (exec:320-364, :631-645, :535-580) plus the k_elem_add
- * residual epilogue (exec:2080-2082). */
+/* y[r] = sum_k W[r][k] x[k] (+ residual[r]); residual and yq may be NULL.
+ * F16 / F32 weights go to m27q_matvec_f32 (yq must then be NULL).  Replaces
+ * l_mv_quant and l_mv_quant_residual (exec:2033-2050, :2089-2104), which
+ * quantize x into the global Q8_1 scratch (l_quant_q8_n, exec:2022-2030)
+ * and then launch the product and the k_elem_add epilogue. */
+M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual,
+                                 void *yq, hipStream_t stream);
+
+/* Same on an already quantized activation.  Replaces l_mv_q8_on
+ * (exec:2054-2083): k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a / k_q80_mv_q8_dp4a
+ * (exec:320-364, :631-645, :535-580) plus the k_elem_add residual epilogue
+ * (exec:2080-2082).  The reference's callers that quantize once and run
+ * several products (the sigmoid-gated quantization in front of Wo, exec:2460,
+ * and K/V on the second stream, exec:2389-2395) map onto this entry point. */
 M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float *y, const float *residual,
                                     void *yq, hipStream_t stream);
 
 /* Up to 4 weights that share one activation (same type, layout, row_blocks),
- * in one launch: y[i] = W[i] xq.  Replaces l_mv_pair (exec:2106-2125) and the
+ * in one launch: y[i] = W[i] x.  Replaces l_mv_pair (exec:2106-2125) and the
  * Wq || Wk, Wv pattern of the attention block (exec:2377-2395). */
+M27Q_API m27q_status m27q_matvec_multi(int n, const m27q_weight *ws, const float *x, float *const *ys,
+                                       hipStream_t stream);
 M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
                                           hipStream_t stream);
 
-/* y[r] = silu(Wg xq)[r] * (Wu xq)[r]; both Q4_K/Q6_K/Q8_0 of one shape.  yq as
- * in m27q_matvec_q8 (may be NULL).  Replaces l_ffn_gate_up_swiglu /
- * k_q4k_q4k_swiglu_dp4a (exec:2239-2261, :369-417). */
-M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const void *xq,
-                                     float *y, void *yq, hipStream_t stream);
+/* y[r] = silu(Wg x)[r] * (Wu x)[r]; gate and up of one type, layout and shape;
+ * yq may be NULL.  Replaces l_ffn_gate_up_swiglu / k_q4k_q4k_swiglu_dp4a
+ * (exec:2239-2261, :369-417), which takes fp32 x. */
+M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const float *x, float *y,
+                                     void *yq, hipStream_t stream);
+M27Q_API m27q_status m27q_ffn_swiglu_q8(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,
+                                        void *yq, hipStream_t stream);
 
 /* fp32-activation product y = W x (+ residual): exact dequantization and fp32
  * accumulation.  Q4_K, Q6_K, Q8_0, F16, F32.  Replaces l_mv_fallback
@@ -157,12 +176,6 @@ M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight 
  * (exec:920-951, :1053-1072, :1076-1096, :899-916, :1100-1114). */
 M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float *y, const float *residual,
                                      hipStream_t stream);
-
-/* Quantize x into scratch (>= m27q_act_bytes(1, K) bytes) and run
- * m27q_matvec_q8; F16/F32 weights go to m27q_matvec_f32.  Replaces l_mv_quant
- * and l_mv_quant_residual (exec:2033-2050, :2089-2104). */
-M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual,
-                                 void *scratch, size_t scratch_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Small-M products (speculative verify / prefill rows)

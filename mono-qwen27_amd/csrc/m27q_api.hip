@@ -74,29 +74,80 @@ int wg_count(int rows) { return ((rows + kTileRows - 1) / kTileRows + kWavesPerW
 
 m27q_status hip_status(hipError_t e) { return e == hipSuccess ? M27Q_OK : M27Q_ERR_HIP; }
 
-void fill_q8_common(GemvParams &p, const m27q_weight *w, const void *xq) {
-    p.rb = (int)w->row_blocks;
-    p.upr = units_per_row(w->ggml_type, w->row_blocks);
-    p.K = k_of(w);
-    const ActView a = act_view(xq, 1, p.K);
-    p.xq = a.q;
-    p.xd = a.d;
-    p.xs = a.s;
+// Launch configuration for a product of upr units per row (m27q_gemv_cfg.h).
+int pick_gemv_cfg(int upr, bool out_quant) {
+    if (out_quant) return kCfgOutQ;
+    if (upr >= 40) return kCfgLongK;
+    if (upr >= 25) return kCfgMidK;
+    return kCfgShortK;
 }
 
 m27q_status check_out_quant(const m27q_weight *w, const void *yq) {
     if (!yq) return M27Q_OK;
     if (!aligned(yq, 16)) return M27Q_ERR_LAYOUT;
-    if (w->row_count % kRowsPerWG) return M27Q_ERR_SHAPE;
+    if (w->row_count % 32) return M27Q_ERR_SHAPE;
     return M27Q_OK;
 }
 
-void fill_out_quant(GemvParams &p, int rows, void *yq) {
-    if (!yq) return;
-    const ActView a = act_view(yq, 1, rows);
-    p.oq = (int8_t *)a.q;
-    p.od = (float *)a.d;
-    p.os = (uint32_t *)a.s;
+// Shared body of every integer-dot M = 1 product.  n weights of one type,
+// layout and K share the activation (fp32 x, or the quantized xq); with
+// swiglu, ws = {gate, up} and ys[0] receives silu(gate x) * (up x).
+m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float *x, float *const *ys,
+                      const float *residual, bool swiglu, void *yq, hipStream_t stream) {
+    if (!ws || !ys) return M27Q_ERR_NULL;
+    if (n < 1 || n > kMaxMulti || (swiglu && n != 2)) return M27Q_ERR_SHAPE;
+    for (int i = 0; i < n; ++i) {
+        const m27q_status st = check_weight(&ws[i], true);
+        if (st != M27Q_OK) return st;
+        if (ws[i].ggml_type != ws[0].ggml_type) return M27Q_ERR_TYPE;
+        if (ws[i].layout != ws[0].layout) return M27Q_ERR_LAYOUT;
+        if (ws[i].row_blocks != ws[0].row_blocks) return M27Q_ERR_SHAPE;
+        if (swiglu && ws[i].row_count != ws[0].row_count) return M27Q_ERR_SHAPE;
+    }
+    const int nout = swiglu ? 1 : n;
+    for (int i = 0; i < nout; ++i)
+        if (!ys[i]) return M27Q_ERR_NULL;
+    if (!xq && !x) return M27Q_ERR_NULL;
+    if (xq && !aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    if (x && !aligned(x, 16)) return M27Q_ERR_LAYOUT;
+    if (yq && nout != 1) return M27Q_ERR_SHAPE;
+    m27q_status st = check_out_quant(&ws[0], yq);
+    if (st != M27Q_OK) return st;
+
+    GemvParams p{};
+    p.rb = (int)ws[0].row_blocks;
+    p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
+    p.K = k_of(&ws[0]);
+    const int cfg = pick_gemv_cfg(p.upr, yq != nullptr);
+    if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
+    if (x) {
+        p.x = x;
+    } else {
+        const ActView a = act_view(xq, 1, p.K);
+        p.xq = a.q;
+        p.xd = a.d;
+        p.xs = a.s;
+    }
+    const int tpw = gemv_q8_tiles_per_wg(cfg);
+    int total = 0;
+    for (int i = 0; i < nout; ++i) {
+        p.W[i] = (const uint8_t *)ws[i].ptr;
+        p.y[i] = ys[i];
+        p.rc[i] = (int)ws[i].row_count;
+        p.wg_start[i] = total;
+        total += (tiles_of(ws[i].row_count) + tpw - 1) / tpw;
+    }
+    if (swiglu) p.W[1] = (const uint8_t *)ws[1].ptr;
+    else p.res[0] = residual;
+    p.wg_start[nout] = total;
+    p.nmat = nout;
+    if (yq) {
+        const ActView a = act_view(yq, 1, (int)ws[0].row_count);
+        p.oq = (int8_t *)a.q;
+        p.od = (float *)a.d;
+        p.os = (uint32_t *)a.s;
+    }
+    return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, swiglu, cfg, p, stream));
 }
 
 }  // namespace
@@ -134,78 +185,21 @@ M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int
 
 M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float *y, const float *residual,
                                     void *yq, hipStream_t stream) {
-    m27q_status st = check_weight(w, true);
-    if (st != M27Q_OK) return st;
-    if (!xq || !y) return M27Q_ERR_NULL;
-    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
-    if ((st = check_out_quant(w, yq)) != M27Q_OK) return st;
-    GemvParams p{};
-    fill_q8_common(p, w, xq);
-    if (gemv_q8_lds_bytes(w->ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
-    const int grid = wg_count((int)w->row_count);
-    p.W[0] = (const uint8_t *)w->ptr;
-    p.y[0] = y;
-    p.res[0] = residual;
-    p.rc[0] = (int)w->row_count;
-    p.wg_start[0] = 0;
-    p.wg_start[1] = grid;
-    p.nmat = 1;
-    fill_out_quant(p, (int)w->row_count, yq);
-    return hip_status(launch_gemv_q8(w->ggml_type, (int)w->layout, false, p, grid, stream));
+    if (!xq) return M27Q_ERR_NULL;
+    return gemv_impl(1, w, xq, nullptr, &y, residual, false, yq, stream);
 }
 
 M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
                                           hipStream_t stream) {
-    if (!ws || !xq || !ys) return M27Q_ERR_NULL;
-    if (n < 1 || n > kMaxMulti) return M27Q_ERR_SHAPE;
-    for (int i = 0; i < n; ++i) {
-        const m27q_status st = check_weight(&ws[i], true);
-        if (st != M27Q_OK) return st;
-        if (!ys[i]) return M27Q_ERR_NULL;
-        if (ws[i].ggml_type != ws[0].ggml_type) return M27Q_ERR_TYPE;
-        if (ws[i].layout != ws[0].layout) return M27Q_ERR_LAYOUT;
-        if (ws[i].row_blocks != ws[0].row_blocks) return M27Q_ERR_SHAPE;
-    }
-    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
-    GemvParams p{};
-    fill_q8_common(p, &ws[0], xq);
-    if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
-    int total = 0;
-    for (int i = 0; i < n; ++i) {
-        p.W[i] = (const uint8_t *)ws[i].ptr;
-        p.y[i] = ys[i];
-        p.rc[i] = (int)ws[i].row_count;
-        p.wg_start[i] = total;
-        total += wg_count((int)ws[i].row_count);
-    }
-    p.wg_start[n] = total;
-    p.nmat = n;
-    return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, false, p, total, stream));
+    if (!xq) return M27Q_ERR_NULL;
+    return gemv_impl(n, ws, xq, nullptr, ys, nullptr, false, nullptr, stream);
 }
 
-M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,
-                                     void *yq, hipStream_t stream) {
-    m27q_status st = check_weight(gate, true);
-    if (st != M27Q_OK) return st;
-    if ((st = check_weight(up, true)) != M27Q_OK) return st;
-    if (!xq || !y) return M27Q_ERR_NULL;
-    if (gate->ggml_type != up->ggml_type) return M27Q_ERR_TYPE;
-    if (gate->layout != up->layout) return M27Q_ERR_LAYOUT;
-    if (gate->row_blocks != up->row_blocks || gate->row_count != up->row_count) return M27Q_ERR_SHAPE;
-    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
-    if ((st = check_out_quant(gate, yq)) != M27Q_OK) return st;
-    GemvParams p{};
-    fill_q8_common(p, gate, xq);
-    if (gemv_q8_lds_bytes(gate->ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
-    const int grid = wg_count((int)gate->row_count);
-    p.W[0] = (const uint8_t *)gate->ptr;
-    p.W[1] = (const uint8_t *)up->ptr;
-    p.y[0] = y;
-    p.rc[0] = (int)gate->row_count;
-    p.wg_start[1] = grid;
-    p.nmat = 1;
-    fill_out_quant(p, (int)gate->row_count, yq);
-    return hip_status(launch_gemv_q8(gate->ggml_type, (int)gate->layout, true, p, grid, stream));
+M27Q_API m27q_status m27q_ffn_swiglu_q8(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,
+                                        void *yq, hipStream_t stream) {
+    if (!gate || !up || !xq) return M27Q_ERR_NULL;
+    const m27q_weight ws[2] = {*gate, *up};
+    return gemv_impl(2, ws, xq, nullptr, &y, nullptr, true, yq, stream);
 }
 
 M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float *y, const float *residual,
@@ -230,18 +224,29 @@ M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float
     return hip_status(launch_gemv_f32(w->ggml_type, (int)w->layout, p, grid, stream));
 }
 
-M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual,
-                                 void *scratch, size_t scratch_bytes, hipStream_t stream) {
+M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y, const float *residual, void *yq,
+                                 hipStream_t stream) {
     const m27q_status st = check_weight(w, false);
     if (st != M27Q_OK) return st;
-    if (!is_quant(w->ggml_type)) return m27q_matvec_f32(w, x, y, residual, stream);
-    if (!x || !y || !scratch) return M27Q_ERR_NULL;
-    const int K = k_of(w);
-    if (scratch_bytes < m27q_act_bytes(1, K)) return M27Q_ERR_SCRATCH;
-    if (!aligned(scratch, 16)) return M27Q_ERR_LAYOUT;
-    const m27q_status q = m27q_quant_act(x, 1, K, scratch, stream);
-    if (q != M27Q_OK) return q;
-    return m27q_matvec_q8(w, scratch, y, residual, nullptr, stream);
+    if (!is_quant(w->ggml_type)) {
+        if (yq) return M27Q_ERR_TYPE;
+        return m27q_matvec_f32(w, x, y, residual, stream);
+    }
+    if (!x) return M27Q_ERR_NULL;
+    return gemv_impl(1, w, nullptr, x, &y, residual, false, yq, stream);
+}
+
+M27Q_API m27q_status m27q_matvec_multi(int n, const m27q_weight *ws, const float *x, float *const *ys,
+                                       hipStream_t stream) {
+    if (!x) return M27Q_ERR_NULL;
+    return gemv_impl(n, ws, nullptr, x, ys, nullptr, false, nullptr, stream);
+}
+
+M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const float *x, float *y,
+                                     void *yq, hipStream_t stream) {
+    if (!gate || !up || !x) return M27Q_ERR_NULL;
+    const m27q_weight ws[2] = {*gate, *up};
+    return gemv_impl(2, ws, nullptr, x, &y, nullptr, true, yq, stream);
 }
 
 M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y, const float *residual,

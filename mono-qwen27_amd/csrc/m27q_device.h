@@ -39,37 +39,88 @@ __device__ __forceinline__ T shfl_xor(T v, int mask, int width = kWave) {
     return __shfl_xor(v, mask, width);
 }
 
-// Sum over the 8 lanes that share one row (lanes 8i .. 8i+7).
+// Cross-lane moves inside a row of 16 lanes (DPP: no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8 lanes
+
+// Sum over 8 consecutive lanes (8a .. 8a+7); every lane gets the sum.
 __device__ __forceinline__ float sum8(float v) {
-    v += shfl_xor(v, 1);
-    v += shfl_xor(v, 2);
-    v += shfl_xor(v, 4);
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
     return v;
 }
 
-// Per-32 activation quantization of one value per lane over 32-lane groups:
-// d = amax/127 (IEEE divide), q = roundf(v/d) clamped to +-127, 0 if amax == 0.
-// Returns the code; *d_out gets d and *s_out the packed 16-lane sums (valid in
-// every lane of the group).
+// ---------------------------------------------------------------------------
+// Per-32 activation quantization.  The rule (fixed here and restated by the
+// oracle): d = amax / 127 (IEEE divide), id = 1 / d (IEEE divide; 0 when
+// d == 0), code = roundf(x * id) (one fp32 multiply, round half away from
+// zero), clamped to +-127.  This is the rule of ggml's reference quantizer
+// quantize_row_q8_1_ref; the reference's GPU kernel (exec:84-107) writes
+// roundf(x / d) under fast-math, which compiles to the same multiply by an
+// approximate reciprocal.  Besides d, the two 16-value integer code sums are
+// kept, packed as (int16 lo) | (int16 hi) << 16.
+__device__ __forceinline__ int quant_code(float x, float id) {
+    const int t = (int)roundf(x * id);
+    return t > 127 ? 127 : (t < -127 ? -127 : t);
+}
+
+__device__ __forceinline__ uint32_t pack_sums(int lo, int hi) {
+    return (uint32_t)(uint16_t)(int16_t)lo | ((uint32_t)(uint16_t)(int16_t)hi << 16);
+}
+
+// One value per lane, one 32-lane half-wave per group.  Returns the code;
+// *d_out gets d and *s_out the packed sums (valid in every lane of the group).
 __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
     float amax = fabsf(v);
 #pragma unroll
-    for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, shfl_xor(amax, m, 32));
+    for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
     const float d = amax / 127.0f;
-    int q = 0;
-    if (amax != 0.0f) {
-        q = (int)roundf(v / d);
-        q = q > 127 ? 127 : (q < -127 ? -127 : q);
-    }
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q = quant_code(v, id);
     int s = q;
 #pragma unroll
-    for (int m = 8; m > 0; m >>= 1) s += shfl_xor(s, m, 16);
+    for (int m = 8; m > 0; m >>= 1) s += __shfl_xor(s, m, 16);
     const int lane32 = (int)(threadIdx.x & 31);
-    const int s_other = shfl_xor(s, 16, 32);
-    const int lo = lane32 < 16 ? s : s_other, hi = lane32 < 16 ? s_other : s;
+    const int s_other = __shfl_xor(s, 16, 32);
     *d_out = d;
-    *s_out = (uint32_t)(uint16_t)(int16_t)lo | ((uint32_t)(uint16_t)(int16_t)hi << 16);
+    *s_out = lane32 < 16 ? pack_sums(s, s_other) : pack_sums(s_other, s);
     return q;
+}
+
+// Eight consecutive values per lane, one group per 4 consecutive lanes
+// (lanes 4a .. 4a+3; lane l of the group holds values 8 l .. 8 l + 7).
+// Returns the 8 codes packed as bytes; *d_out and *s_out as in quant32.
+// Bit-identical to quant32 on the same group: the max, the divides, the
+// multiplies and the integer sums see the same values.
+__device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uint32_t *s_out) {
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                       fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+    amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = quant_code(a.x, id), q1 = quant_code(a.y, id), q2 = quant_code(a.z, id), q3 = quant_code(a.w, id);
+    const int q4 = quant_code(b.x, id), q5 = quant_code(b.y, id), q6 = quant_code(b.z, id), q7 = quant_code(b.w, id);
+    int s = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
+    s += dpp_i<kDppXor1>(s);  // lanes 0-1: values 0..15; lanes 2-3: values 16..31
+    const int s_other = dpp_i<kDppXor2>(s);
+    *d_out = d;
+    *s_out = (threadIdx.x & 2) == 0 ? pack_sums(s, s_other) : pack_sums(s_other, s);
+    const uint32_t w0 = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                        ((uint32_t)q3 << 24);
+    const uint32_t w1 = (uint32_t)(q4 & 0xff) | ((uint32_t)(q5 & 0xff) << 8) | ((uint32_t)(q6 & 0xff) << 16) |
+                        ((uint32_t)q7 << 24);
+    return make_uint2(w0, w1);
 }
 
 }  // namespace m27q

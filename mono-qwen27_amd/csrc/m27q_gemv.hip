@@ -1,26 +1,279 @@
 // m27q_gemv.hip -- M = 1 matrix-vector products on gfx950.
 //
-// One workgroup = 4 wavefronts = 32 output rows; each wavefront owns a tile of
-// 8 rows and streams its weight tile unit by unit (one 256-weight block
-// column, or four Q8_0 block columns) with 16-byte loads per lane.  The
-// activation is staged once per workgroup in LDS; every lane of a row reads
-// its 32 activation codes from there (8 distinct addresses per instruction).
-// Loads run two pipeline stages of kDepth units ahead of the arithmetic.
-// The 8 partial sums of a row are combined with cross-lane adds at the end.
+// Integer-dot products (int8 activation codes x GGUF weight codes):
+//   A workgroup owns TPW tiles of 8 rows and KS wavefronts.  Wave w streams the
+//   w-th K slice (a contiguous run of units) of every one of those tiles,
+//   unit by unit: for each unit it reads the activation fragment from LDS once
+//   and applies it to the unit's block in all TPW tiles.  The loads of the
+//   next unit (TPW fragments per matrix) are issued before the current unit is
+//   computed (double buffering); every load in the loop is unconditional, so
+//   the number of loads in flight at each wait is fixed at compile time.
+//   Splitting K over the waves multiplies the number of wavefronts a short
+//   matrix launches (the 5120-row down projection launches 640 x KS waves
+//   instead of 640).  Within a wave, lane 8 i + c works on row i of a tile and
+//   on the c-th 16-byte chunk of the unit's quants; the 8 lane partials of a
+//   row are combined with DPP adds, the KS wave partials in LDS, in a fixed
+//   order (the result does not depend on timing).
+//   The activation is staged once per workgroup in LDS: either copied from an
+//   already quantized buffer, or quantized right there from fp32 values with
+//   the rule of m27q_quant_act (same codes, bit for bit), which removes the
+//   separate quantization launch in front of every product.  Its loads are
+//   issued before the first weight loads.
+//   Epilogues: + residual, SwiGLU of two matrices (silu(gate) * up), and the
+//   per-32 quantization of the output rows for the next product.
+//
+// fp32-activation products (exact dequantization, fp32 accumulation) keep the
+// simpler one-wave-per-tile mapping: they are the fallback, not the hot path.
 //
 // Replaces k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a / k_q80_mv_q8_dp4a
-// (exec:320-364, :631-645, :535-580), k_q4k_q4k_swiglu_dp4a (exec:369-417)
-// and the fp32 fallbacks k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv / k_f32_mv
-// (exec:920-951, :1053-1072, :1076-1096, :899-916, :1100-1114).
+// (exec:320-364, :631-645, :535-580), k_q4k_q4k_swiglu_dp4a (exec:369-417),
+// k_quant_q8_1 in front of them (exec:84-107, launched by l_quant_q8_n
+// :2022-2030) and the fp32 fallbacks k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv
+// / k_f32_mv (exec:920-951, :1053-1072, :1076-1096, :899-916, :1100-1114).
+#include "m27q_gemv_cfg.h"
 #include "m27q_internal.h"
 #include "m27q_types.h"
 
 namespace m27q {
 
-template <class T>
-__device__ __forceinline__ int padded_k(int upr) {
-    return upr * T::kUnitElems;
+// Activation staging into LDS: codes[Kp] | d[Kp/32] | aux[Kp/32] (zero
+// padded from K to Kp).  stage_issue() loads the first batch into registers;
+// stage_finish() converts and stores it, then handles any further batches.
+constexpr int kStageSlots = 4;  // per thread: 4 x 32 B of fp32 values, or 4 x 16 B of codes
+
+template <bool XF32>
+struct StageRegs {
+    float4 v[kStageSlots][2];
+};
+template <>
+struct StageRegs<false> {
+    uint4 v[kStageSlots];
+    float d[kStageSlots];
+    uint32_t s[kStageSlots];
+};
+
+template <bool XF32>
+__device__ __forceinline__ void stage_load(StageRegs<XF32> &r, const GemvParams &p, int j0, int nth) {
+    if constexpr (XF32) {
+        // slot b of thread t: values 8 j .. 8 j + 7 with j = j0 + b * nth
+        const int k8 = p.K / 8;
+        const float4 *x4 = (const float4 *)p.x;
+#pragma unroll
+        for (int b = 0; b < kStageSlots; ++b) {
+            const int j = j0 + b * nth;
+            const bool in = j < k8;
+            r.v[b][0] = in ? x4[2 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            r.v[b][1] = in ? x4[2 * j + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    } else {
+        const int k16 = p.K / 16, k32 = p.K / 32;
+        const uint4 *src = (const uint4 *)p.xq;
+#pragma unroll
+        for (int b = 0; b < kStageSlots; ++b) {
+            const int j = j0 + b * nth;
+            r.v[b] = j < k16 ? src[j] : make_uint4(0, 0, 0, 0);
+            r.d[b] = j < k32 ? p.xd[j] : 0.f;
+            r.s[b] = j < k32 ? p.xs[j] : 0u;
+        }
+    }
 }
+
+template <class T, bool XF32>
+__device__ __forceinline__ void stage_store(const StageRegs<XF32> &r, uint8_t *smem, int Kp, int j0, int nth) {
+    int8_t *xc = (int8_t *)smem;
+    float *xd = (float *)(smem + Kp);
+    uint32_t *xs = (uint32_t *)(smem + Kp + Kp / 8);
+    if constexpr (XF32) {
+        // A 32-value group is 4 consecutive slots j (4 consecutive lanes; nth
+        // and Kp / 8 are multiples of 4, so a group is wholly in or out).
+#pragma unroll
+        for (int b = 0; b < kStageSlots; ++b) {
+            const int j = j0 + b * nth;
+            if (j < Kp / 8) {
+                float d;
+                uint32_t s;
+                ((uint2 *)xc)[j] = quant32x8(r.v[b][0], r.v[b][1], &d, &s);
+                if ((j & 3) == 0) {
+                    xd[j / 4] = d;
+                    xs[j / 4] = T::stage_aux(d, s);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < kStageSlots; ++b) {
+            const int j = j0 + b * nth;
+            if (j < Kp / 16) ((uint4 *)xc)[j] = r.v[b];
+            if (j < Kp / 32) {
+                xd[j] = r.d[b];
+                xs[j] = T::stage_aux(r.d[b], r.s[b]);
+            }
+        }
+    }
+}
+
+template <bool XF32>
+__device__ __forceinline__ int stage_span(int Kp) {
+    return XF32 ? Kp / 8 : Kp / 16;  // slots needed for the whole activation
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Weight fragments of one unit for the TPW tiles of every matrix.
+template <class T, int LAYOUT, int NM, int TPW>
+struct UnitStream {
+    const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
+    int i, c, rb;
+    typename T::Lane L;
+
+    __device__ UnitStream(const uint8_t *const *W, int tile0, int ntiles, int rc, int rb_, int upr, int lane)
+        : i(lane >> 3), c(lane & 7), rb(rb_), L(lane & 7) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int t = 0; t < TPW; ++t) {
+                const int tile = min(tile0 + t, ntiles - 1);  // past the end: reread the last tile
+                if constexpr (LAYOUT == M27Q_LAYOUT_TILED) {
+                    base[m][t] = W[m] + (size_t)tile * upr * T::kUnitBytes;
+                } else {
+                    const int row = min(tile * kTileRows + i, rc - 1);
+                    base[m][t] = W[m] + (size_t)row * rb_ * T::kBlockBytes;
+                }
+            }
+    }
+
+    __device__ void load(typename T::Frag (&f)[NM][TPW], int u) const {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int t = 0; t < TPW; ++t) {
+                if constexpr (LAYOUT == M27Q_LAYOUT_TILED)
+                    f[m][t] = T::load_tiled(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
+                else
+                    f[m][t] = T::load_gguf(base[m][t], u, rb, c, L);
+            }
+    }
+};
+
+template <class T, int NM, int TPW>
+__device__ __forceinline__ void compute_unit(const typename T::Frag (&f)[NM][TPW], const ActLds &act, int u,
+                                             const typename T::Lane &L, float (&acc)[NM][TPW]) {
+    const typename T::AFrag a = T::load_act(act, u, L);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) acc[m][t] += T::dot(f[m][t], a, L);
+}
+
+template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>
+__global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int KS = C::KS, TPW = C::TPW;
+    constexpr int NM = SWIGLU ? 2 : 1;
+    constexpr int NR = TPW * kTileRows;  // rows per workgroup
+    const int lane = (int)(threadIdx.x & 63), i = lane >> 3, c = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nth = KS * kWave;
+
+    // Matrix of this workgroup (up to kMaxMulti matrices share one launch).
+    int m = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMulti; ++k)
+        if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) m = k;
+    const int rc = p.rc[m];
+    const int tile0 = ((int)blockIdx.x - p.wg_start[m]) * TPW;
+    const int ntiles = (rc + kTileRows - 1) / kTileRows;
+
+    // K slice of this wave: units [ub, ub + nu); a wave with no units reads a
+    // valid unit and discards it.
+    const int U = p.upr / KS, rem = p.upr % KS;
+    const int ub = wave * U + min(wave, rem);
+    const int nu = U + (wave < rem ? 1 : 0);
+
+    // 1. first batch of the activation, 2. the first unit of weights (their
+    // latency overlaps the staging), 3. activation to LDS.
+    const int Kp = p.upr * T::kUnitElems;
+    StageRegs<XF32> sr;
+    stage_load<XF32>(sr, p, (int)threadIdx.x, nth);
+
+    const uint8_t *W[NM];
+    W[0] = p.W[m];
+    if constexpr (SWIGLU) W[NM - 1] = p.W[1];
+    const UnitStream<T, LAYOUT, NM, TPW> ws(W, tile0, ntiles, rc, p.rb, p.upr, lane);
+    typename T::Frag fa[NM][TPW], fb[NM][TPW];
+    ws.load(fa, min(ub, p.upr - 1));
+
+    stage_store<T, XF32>(sr, smem, Kp, (int)threadIdx.x, nth);
+    for (int j0 = (int)threadIdx.x + kStageSlots * nth; j0 < stage_span<XF32>(Kp); j0 += kStageSlots * nth) {
+        stage_load<XF32>(sr, p, j0, nth);
+        stage_store<T, XF32>(sr, smem, Kp, j0, nth);
+    }
+    const ActLds act{(const int8_t *)smem, (const float *)(smem + Kp), (const uint32_t *)(smem + Kp + Kp / 8)};
+    float *red = (float *)(smem + Kp + Kp / 4);  // [NM][KS][NR]
+    __syncthreads();
+
+    float acc[NM][TPW];
+#pragma unroll
+    for (int mm = 0; mm < NM; ++mm)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) acc[mm][t] = 0.f;
+    int k = 0;
+    for (; k + 2 < nu; k += 2) {
+        ws.load(fb, ub + k + 1);
+        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
+        ws.load(fa, ub + k + 2);
+        compute_unit<T, NM, TPW>(fb, act, ub + k + 1, ws.L, acc);
+    }
+    if (k + 1 < nu) {
+        ws.load(fb, ub + k + 1);
+        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
+        compute_unit<T, NM, TPW>(fb, act, ub + k + 1, ws.L, acc);
+    } else if (k < nu) {
+        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
+    }
+
+    // Row partials of this wave's slice -> LDS.
+#pragma unroll
+    for (int mm = 0; mm < NM; ++mm)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            const float r = sum8(acc[mm][t]);
+            if (c == 0) red[(mm * KS + wave) * NR + t * kTileRows + i] = r;
+        }
+    __syncthreads();
+
+    // Epilogue: one thread per row of the workgroup.
+    const int t = (int)threadIdx.x;
+    if (t < NR) {
+        const int row = tile0 * kTileRows + t;
+        float v = red[t];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) v += red[w * NR + t];
+        if constexpr (SWIGLU) {
+            float vu = red[KS * NR + t];
+#pragma unroll
+            for (int w = 1; w < KS; ++w) vu += red[(KS + w) * NR + t];
+            v = silu(v) * vu;
+        } else {
+            if (p.res[m] && row < rc) v += p.res[m][row];
+        }
+        if (row < rc) p.y[m][row] = v;
+        // Fused per-32 quantization of the output (rc % 32 == 0 and NR % 32 == 0
+        // are checked on the host, so a 32-row group is wholly in or out).
+        if (p.oq && tile0 * kTileRows + (t & ~31) < rc) {
+            float d;
+            uint32_t s;
+            const int q = quant32(v, &d, &s);
+            p.oq[row] = (int8_t)q;
+            if ((t & 31) == 0) {
+                p.od[row / 32] = d;
+                p.os[row / 32] = s;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------ fp32-activation products --
 
 // Weight-tile iterator: per wave, yields fragment loads for unit u.
 template <class T, int LAYOUT>
@@ -39,9 +292,9 @@ struct TileSrc {
     }
 };
 
-// acc += sum over units of T::dot (or dot_f32) with a two-stage load pipeline.
-template <class T, int LAYOUT, int kDepth, bool F32, class A>
-__device__ __forceinline__ float stream_row(const TileSrc<T, LAYOUT> &src, const A &act, int upr) {
+// acc += sum over units of T::dot_f32 with a two-stage load pipeline.
+template <class T, int LAYOUT, int kDepth, class A>
+__device__ __forceinline__ float stream_row_f32(const TileSrc<T, LAYOUT> &src, const A &act, int upr) {
     typename T::Frag fa[kDepth], fb[kDepth];
     float acc = 0.f;
 #pragma unroll
@@ -53,112 +306,22 @@ __device__ __forceinline__ float stream_row(const TileSrc<T, LAYOUT> &src, const
             if (u0 + kDepth + k < upr) fb[k] = src.load(u0 + kDepth + k);
 #pragma unroll
         for (int k = 0; k < kDepth; ++k)
-            if (u0 + k < upr) {
-                if constexpr (F32) acc += T::dot_f32(fa[k], act, u0 + k, src.L);
-                else acc += T::dot(fa[k], act, u0 + k, src.L);
-            }
+            if (u0 + k < upr) acc += T::dot_f32(fa[k], act, u0 + k, src.L);
 #pragma unroll
         for (int k = 0; k < kDepth; ++k)
             if (u0 + 2 * kDepth + k < upr) fa[k] = src.load(u0 + 2 * kDepth + k);
 #pragma unroll
         for (int k = 0; k < kDepth; ++k)
-            if (u0 + kDepth + k < upr) {
-                if constexpr (F32) acc += T::dot_f32(fb[k], act, u0 + kDepth + k, src.L);
-                else acc += T::dot(fb[k], act, u0 + kDepth + k, src.L);
-            }
+            if (u0 + kDepth + k < upr) acc += T::dot_f32(fb[k], act, u0 + kDepth + k, src.L);
     }
     return acc;
 }
 
-// Stage the quantized activation (global -> LDS), zero-padding to Kp.
-template <class T>
-__device__ __forceinline__ ActLds stage_act_q8(uint8_t *smem, const GemvParams &p, int Kp) {
-    int8_t *xc = (int8_t *)smem;
-    float *xd = (float *)(smem + Kp);
-    uint32_t *xs = (uint32_t *)(smem + Kp + Kp / 8);
-    const uint4 *src = (const uint4 *)p.xq;
-    for (int j = threadIdx.x; j < Kp / 16; j += blockDim.x)
-        ((uint4 *)xc)[j] = (j < p.K / 16) ? src[j] : make_uint4(0, 0, 0, 0);
-    for (int j = threadIdx.x; j < Kp / 32; j += blockDim.x) {
-        float d = 0.f;
-        uint32_t s = 0u;
-        if (j < p.K / 32) {
-            d = p.xd[j];
-            s = p.xs[j];
-        }
-        xd[j] = d;
-        xs[j] = T::stage_aux(d, s);
-    }
-    return {xc, xd, xs};
-}
-
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
-// Fused epilogue: quantize the workgroup's 32 consecutive outputs (row0 .. row0+31).
-__device__ __forceinline__ void quant_epilogue(float *outv, const GemvParams &p, int wave, int i, int c,
-                                               float v, int row0) {
-    if (c == 0) outv[wave * kTileRows + i] = v;
-    __syncthreads();
-    if (threadIdx.x < 32) {
-        float d;
-        uint32_t s;
-        const int q = quant32(outv[threadIdx.x], &d, &s);
-        p.oq[row0 + threadIdx.x] = (int8_t)q;
-        if (threadIdx.x == 0) {
-            p.od[row0 / 32] = d;
-            p.os[row0 / 32] = s;
-        }
-    }
-}
-
-template <class T, int LAYOUT, bool SWIGLU>
-__global__ __launch_bounds__(256) void k_gemv_q8(GemvParams p) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int Kp = padded_k<T>(p.upr);
-    const ActLds act = stage_act_q8<T>(smem, p, Kp);
-    float *outv = (float *)(smem + Kp + Kp / 4);
-    __syncthreads();
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane >> 3, c = lane & 7;
-    int m = 0;
-#pragma unroll
-    for (int k = 1; k < kMaxMulti; ++k)
-        if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) m = k;
-    const int wgl = (int)blockIdx.x - p.wg_start[m];
-    const int rc = p.rc[m];
-    const int tile = wgl * kWavesPerWG + wave;
-    const int ntiles = (rc + kTileRows - 1) / kTileRows;
-    const int row = tile * kTileRows + i;
-    const int row_ld = row < rc ? row : rc - 1;  // GGUF rows past the end: reread the last row
-
-    float acc = 0.f, acc_up = 0.f;
-    if (tile < ntiles) {
-        constexpr int kDepth = SWIGLU ? 2 : 4;
-        const TileSrc<T, LAYOUT> src(p.W[m], tile, row_ld, p.rb, p.upr, lane);
-        acc = stream_row<T, LAYOUT, kDepth, false>(src, act, p.upr);
-        if constexpr (SWIGLU) {
-            const TileSrc<T, LAYOUT> src_up(p.W[1], tile, row_ld, p.rb, p.upr, lane);
-            acc_up = stream_row<T, LAYOUT, kDepth, false>(src_up, act, p.upr);
-        }
-    }
-    acc = sum8(acc);
-    float v;
-    if constexpr (SWIGLU) {
-        acc_up = sum8(acc_up);
-        v = silu(acc) * acc_up;
-    } else {
-        v = acc;
-        if (p.res[m] && tile < ntiles && row < rc) v += p.res[m][row];
-    }
-    if (c == 0 && tile < ntiles && row < rc) p.y[m][row] = v;
-    if (p.oq) quant_epilogue(outv, p, wave, i, c, v, wgl * kRowsPerWG);
-}
-
-// fp32-activation product: stage x and its per-16 sums in LDS.
+// One workgroup = 4 waves = 32 rows; x and its per-16 sums staged in LDS.
 template <class T, int LAYOUT>
 __global__ __launch_bounds__(256) void k_gemv_f32(GemvParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int Kp = padded_k<T>(p.upr);
+    const int Kp = p.upr * T::kUnitElems;
     float *xf = (float *)smem;
     float *x16 = xf + Kp;
     for (int j = threadIdx.x; j < Kp / 4; j += blockDim.x)
@@ -182,7 +345,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(GemvParams p) {
     float acc = 0.f;
     if (tile < ntiles) {
         const TileSrc<T, LAYOUT> src(p.W[0], tile, row_ld, p.rb, p.upr, lane);
-        acc = stream_row<T, LAYOUT, 2, true>(src, act, p.upr);
+        acc = stream_row_f32<T, LAYOUT, 2>(src, act, p.upr);
     }
     acc = sum8(acc);
     if (c == 0 && tile < ntiles && row < rc) p.y[0][row] = acc + (p.res[0] ? p.res[0][row] : 0.f);
@@ -222,42 +385,84 @@ __global__ __launch_bounds__(256) void k_gemv_dense(GemvParams p) {
 
 // ------------------------------------------------------------- launchers --
 
-template <class T, int LAYOUT, bool SWIGLU>
-static hipError_t launch_q8(const GemvParams &p, int grid, hipStream_t s) {
-    const int Kp = p.upr * T::kUnitElems;
-    const size_t lds = (size_t)Kp + (size_t)Kp / 4 + kRowsPerWG * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q8<T, LAYOUT, SWIGLU>), dim3(grid), dim3(256), lds, s, p);
+template <class T, class C, bool SWIGLU>
+size_t gemv_q8_lds(int upr) {
+    const size_t Kp = (size_t)upr * T::kUnitElems;
+    return Kp + Kp / 4 + (size_t)(SWIGLU ? 2 : 1) * C::KS * C::TPW * kTileRows * sizeof(float);
+}
+
+template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>
+static hipError_t launch_q8_cfg(const GemvParams &p, hipStream_t s) {
+    const size_t lds = gemv_q8_lds<T, C, SWIGLU>(p.upr);
+    hipLaunchKernelGGL((k_gemv_q8<T, LAYOUT, C, SWIGLU, XF32>), dim3(p.wg_start[p.nmat]), dim3(kWave * C::KS), lds, s,
+                       p);
     return hipGetLastError();
 }
 
-template <class T, bool SWIGLU>
-static hipError_t dispatch_layout_q8(const GemvParams &p, int layout, int grid, hipStream_t s) {
-    return layout == M27Q_LAYOUT_TILED ? launch_q8<T, M27Q_LAYOUT_TILED, SWIGLU>(p, grid, s)
-                                       : launch_q8<T, M27Q_LAYOUT_GGUF, SWIGLU>(p, grid, s);
+template <class T, int LAYOUT, bool SWIGLU, bool XF32>
+static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
+    switch (cfg) {
+        case kCfgLongK: return launch_q8_cfg<T, LAYOUT, CfgLongK, SWIGLU, XF32>(p, s);
+        case kCfgMidK: return launch_q8_cfg<T, LAYOUT, CfgMidK, SWIGLU, XF32>(p, s);
+        case kCfgOutQ: return launch_q8_cfg<T, LAYOUT, CfgOutQ, SWIGLU, XF32>(p, s);
+        default: return launch_q8_cfg<T, LAYOUT, CfgShortK, SWIGLU, XF32>(p, s);
+    }
 }
 
-size_t gemv_q8_lds_bytes(uint32_t type, int upr) {
-    const int ue = type == kQ8_0 ? Q80::kUnitElems : 256;
-    const size_t Kp = (size_t)upr * ue;
-    return Kp + Kp / 4 + kRowsPerWG * sizeof(float);
+template <class T, bool SWIGLU, bool XF32>
+static hipError_t launch_q8_l(const GemvParams &p, int layout, int cfg, hipStream_t s) {
+    return layout == M27Q_LAYOUT_TILED ? launch_q8_t<T, M27Q_LAYOUT_TILED, SWIGLU, XF32>(p, cfg, s)
+                                       : launch_q8_t<T, M27Q_LAYOUT_GGUF, SWIGLU, XF32>(p, cfg, s);
+}
+
+template <class T>
+static hipError_t launch_q8_x(const GemvParams &p, int layout, bool swiglu, int cfg, hipStream_t s) {
+    const bool xf = p.x != nullptr;
+    if (swiglu) return xf ? launch_q8_l<T, true, true>(p, layout, cfg, s) : launch_q8_l<T, true, false>(p, layout, cfg, s);
+    return xf ? launch_q8_l<T, false, true>(p, layout, cfg, s) : launch_q8_l<T, false, false>(p, layout, cfg, s);
+}
+
+template <class T>
+static size_t lds_for(int upr, bool swiglu, int cfg) {
+    switch (cfg) {
+        case kCfgLongK: return swiglu ? gemv_q8_lds<T, CfgLongK, true>(upr) : gemv_q8_lds<T, CfgLongK, false>(upr);
+        case kCfgMidK: return swiglu ? gemv_q8_lds<T, CfgMidK, true>(upr) : gemv_q8_lds<T, CfgMidK, false>(upr);
+        case kCfgOutQ: return swiglu ? gemv_q8_lds<T, CfgOutQ, true>(upr) : gemv_q8_lds<T, CfgOutQ, false>(upr);
+        default: return swiglu ? gemv_q8_lds<T, CfgShortK, true>(upr) : gemv_q8_lds<T, CfgShortK, false>(upr);
+    }
+}
+
+size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg) {
+    switch (type) {
+        case kQ4_K: return lds_for<Q4K>(upr, swiglu, cfg);
+        case kQ6_K: return lds_for<Q6K>(upr, swiglu, cfg);
+        case kQ8_0: return lds_for<Q80>(upr, swiglu, cfg);
+        default: return 0;
+    }
+}
+
+int gemv_q8_tiles_per_wg(int cfg) {
+    switch (cfg) {
+        case kCfgLongK: return CfgLongK::TPW;
+        case kCfgMidK: return CfgMidK::TPW;
+        case kCfgOutQ: return CfgOutQ::TPW;
+        default: return CfgShortK::TPW;
+    }
+}
+
+hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, int cfg, const GemvParams &p, hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_q8_x<Q4K>(p, layout, swiglu, cfg, s);
+        case kQ6_K: return launch_q8_x<Q6K>(p, layout, swiglu, cfg, s);
+        case kQ8_0: return launch_q8_x<Q80>(p, layout, swiglu, cfg, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 size_t gemv_f32_lds_bytes(uint32_t type, int upr) {
     const int ue = type == kQ8_0 ? Q80::kUnitElems : 256;
     const size_t Kp = (size_t)upr * ue;
     return Kp * 4 + Kp / 4;
-}
-
-hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, const GemvParams &p, int grid, hipStream_t s) {
-    switch (type) {
-        case kQ4_K: return swiglu ? dispatch_layout_q8<Q4K, true>(p, layout, grid, s)
-                                  : dispatch_layout_q8<Q4K, false>(p, layout, grid, s);
-        case kQ6_K: return swiglu ? dispatch_layout_q8<Q6K, true>(p, layout, grid, s)
-                                  : dispatch_layout_q8<Q6K, false>(p, layout, grid, s);
-        case kQ8_0: return swiglu ? dispatch_layout_q8<Q80, true>(p, layout, grid, s)
-                                  : dispatch_layout_q8<Q80, false>(p, layout, grid, s);
-        default: return hipErrorInvalidValue;
-    }
 }
 
 template <class T, int LAYOUT>

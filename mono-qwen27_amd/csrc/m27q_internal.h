@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "../../include/m27q.h"
+#include "m27q_gemv_cfg.h"
 #include "m27q_layout.h"
 
 namespace m27q {
@@ -35,9 +36,13 @@ struct GemvParams {
     uint32_t *os;
 };
 
-size_t gemv_q8_lds_bytes(uint32_t type, int upr);
+// Integer-dot GEMV (m27q_gemv.hip).  cfg: kCfgShortK / kCfgMidK / kCfgLongK
+// (m27q_gemv_cfg.h).  The grid is p.wg_start[p.nmat] workgroups.  The
+// activation is p.x (fp32, quantized in the kernel) when not NULL, else p.xq.
+size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg);
+int gemv_q8_tiles_per_wg(int cfg);
+hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, int cfg, const GemvParams &p, hipStream_t s);
 size_t gemv_f32_lds_bytes(uint32_t type, int upr);
-hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, const GemvParams &p, int grid, hipStream_t s);
 hipError_t launch_gemv_f32(uint32_t type, int layout, const GemvParams &p, int grid, hipStream_t s);
 
 hipError_t launch_quant_act(const float *x, const float *gate, long long n, int8_t *q, float *d, uint32_t *s,

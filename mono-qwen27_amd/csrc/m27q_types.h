@@ -55,6 +55,10 @@ struct Q4K {
     struct Lane {
         int c, g, off, shA, shm;
         bool gl, cl;
+        // Branch-free decode of the 6-bit scales (get_scale_min_k4, exec:690-693):
+        // sc pair = ((X >> sx) & sm) | ((h.y >> sy) & sh) with X = h.y (g < 2) or h.w,
+        // min     = ((Y >> mx) & mm) | ((h.z >> my) & mh) with Y = h.z (c < 4) or h.w.
+        uint32_t sx, sm, sy, shm6, mx, mm, my, mh;
         __device__ explicit Lane(int c_) : c(c_) {
             g = c >> 1;
             off = 64 * g + 16 * (c & 1);
@@ -62,7 +66,23 @@ struct Q4K {
             shm = 8 * (c & 3);
             gl = g < 2;
             cl = c < 4;
+            sx = shA;
+            sm = gl ? 0x3f3fu : 0x0f0fu;
+            sy = shA + 2;
+            shm6 = gl ? 0u : 0x3030u;
+            mx = cl ? shm : shm + 4;
+            mm = cl ? 63u : 15u;
+            my = shm + 2;
+            mh = cl ? 0u : 0x30u;
         }
+    };
+
+    // Activation fragment of one unit for lane c: its 2 x 16 codes, the scales
+    // of its two 32-groups, and d * (code sum) of group c for the min term.
+    struct AFrag {
+        int4 lo, hi;
+        float2 dx;
+        float dsum;
     };
 
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
@@ -73,15 +93,14 @@ struct Q4K {
         return {ld_u128(blk + kQ4KHdr + 16 * c), ld_u128(blk)};
     }
 
-    // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c:
-    // get_scale_min_k4 (exec:690-693) evaluated on the packed dwords directly.
+    // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c.
     __device__ static uint32_t scale_pair(const uint4 &h, const Lane &L) {
-        return L.gl ? ((h.y >> L.shA) & 0x3f3fu)
-                    : (((h.w >> L.shA) & 0x0f0fu) | ((h.y >> (L.shA + 2)) & 0x3030u));
+        const uint32_t X = L.gl ? h.y : h.w;
+        return ((X >> L.sx) & L.sm) | ((h.y >> L.sy) & L.shm6);
     }
     __device__ static int min_c(const uint4 &h, const Lane &L) {
-        return (int)(L.cl ? ((h.z >> L.shm) & 63u)
-                          : (((h.w >> (L.shm + 4)) & 15u) | ((h.z >> (L.shm + 2)) & 0x30u)));
+        const uint32_t Y = L.cl ? h.z : h.w;
+        return (int)(((Y >> L.mx) & L.mm) | ((h.z >> L.my) & L.mh));
     }
 
     // LDS aux word: d * (sum of the 32 codes), the scale of the block-min term.
@@ -90,24 +109,35 @@ struct Q4K {
         return __float_as_uint(d * (float)S);
     }
 
-    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
-        const int4 alo = *(const int4 *)(a.xc + 256 * u + L.off);
-        const int4 ahi = *(const int4 *)(a.xc + 256 * u + L.off + 32);
-        int slo = dot4((int)(f.q.x & kM4), alo.x, 0);
-        slo = dot4((int)(f.q.y & kM4), alo.y, slo);
-        slo = dot4((int)(f.q.z & kM4), alo.z, slo);
-        slo = dot4((int)(f.q.w & kM4), alo.w, slo);
-        int shi = dot4((int)((f.q.x >> 4) & kM4), ahi.x, 0);
-        shi = dot4((int)((f.q.y >> 4) & kM4), ahi.y, shi);
-        shi = dot4((int)((f.q.z >> 4) & kM4), ahi.z, shi);
-        shi = dot4((int)((f.q.w >> 4) & kM4), ahi.w, shi);
+    __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
+        AFrag r;
+        r.lo = *(const int4 *)(a.xc + 256 * u + L.off);
+        r.hi = *(const int4 *)(a.xc + 256 * u + L.off + 32);
+        r.dx = *(const float2 *)(a.xd + 8 * u + 2 * L.g);
+        r.dsum = __uint_as_float(a.xs[8 * u + L.c]);
+        return r;
+    }
+
+    // Per 32-group j of the block: d sc_j dx_j sum(q4 q8) - dmin m_j dx_j sum(q8)
+    // (the vec_dot_q4_K_q8_1 terms, exec:250-310), for this lane's share.
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
+        int slo = dot4((int)(f.q.x & kM4), a.lo.x, 0);
+        slo = dot4((int)(f.q.y & kM4), a.lo.y, slo);
+        slo = dot4((int)(f.q.z & kM4), a.lo.z, slo);
+        slo = dot4((int)(f.q.w & kM4), a.lo.w, slo);
+        int shi = dot4((int)((f.q.x >> 4) & kM4), a.hi.x, 0);
+        shi = dot4((int)((f.q.y >> 4) & kM4), a.hi.y, shi);
+        shi = dot4((int)((f.q.z >> 4) & kM4), a.hi.z, shi);
+        shi = dot4((int)((f.q.w >> 4) & kM4), a.hi.w, shi);
         const uint32_t pair = scale_pair(f.h, L);
         const int m = min_c(f.h, L);
-        const float2 dx = *(const float2 *)(a.xd + 8 * u + 2 * L.g);
-        const float dsum = __uint_as_float(a.xs[8 * u + L.c]);
+        // |code sums| < 2^16 and scales < 2^6: the 24-bit products are exact.
+        const float t = fmaf(a.dx.y, (float)__mul24((int)(pair >> 8), shi), a.dx.x * (float)__mul24((int)(pair & 0xffu), slo));
         const float dw = f16_bits_to_f32(f.h.x), dm = f16_bits_to_f32(f.h.x >> 16);
-        const float t = dx.x * (float)((int)(pair & 0xffu) * slo) + dx.y * (float)((int)(pair >> 8) * shi);
-        return dw * t - dm * ((float)m * dsum);
+        return fmaf(dw, t, -dm * ((float)m * a.dsum));
+    }
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        return dot(f, load_act(a, u, L), L);
     }
 
     __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
@@ -198,26 +228,49 @@ struct Q6K {
         return hi ? (int)(int16_t)(s >> 16) : (int)(int16_t)(s & 0xffffu);
     }
 
-    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+    // Activation fragment of one unit for lane c: 2 x 16 codes, their scales,
+    // and 32 x (code sums): the weight codes are q + 32, so the offset is
+    // removed exactly with these integer sums.
+    struct AFrag {
+        int4 lo, hi;
+        float dlo, dhi;
+        int olo, ohi;
+    };
+
+    __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
+        AFrag r;
+        r.lo = *(const int4 *)(a.xc + 256 * u + L.aoff);
+        r.hi = *(const int4 *)(a.xc + 256 * u + L.aoff + 64);
+        const int jl = 8 * u + L.jlo;
+        r.dlo = a.xd[jl];
+        r.dhi = a.xd[jl + 2];
+        r.olo = 32 * s16(a.xs[jl], L.hsel);
+        r.ohi = 32 * s16(a.xs[jl + 2], L.hsel);
+        return r;
+    }
+
+    // Per 16-group j: d sc_j dx_(j/2) sum((q6 - 32) q8) (vec_dot_q6_K_q8_1, exec:586-628).
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
         uint32_t lo6[4], hi6[4];
         codes(f, L, lo6, hi6);
-        const int4 alo = *(const int4 *)(a.xc + 256 * u + L.aoff);
-        const int4 ahi = *(const int4 *)(a.xc + 256 * u + L.aoff + 64);
-        int slo = dot4((int)lo6[0], alo.x, 0);
-        slo = dot4((int)lo6[1], alo.y, slo);
-        slo = dot4((int)lo6[2], alo.z, slo);
-        slo = dot4((int)lo6[3], alo.w, slo);
-        int shi = dot4((int)hi6[0], ahi.x, 0);
-        shi = dot4((int)hi6[1], ahi.y, shi);
-        shi = dot4((int)hi6[2], ahi.z, shi);
-        shi = dot4((int)hi6[3], ahi.w, shi);
-        const int jl = 8 * u + L.jlo;
-        slo -= 32 * s16(a.xs[jl], L.hsel);      // codes are q+32: remove the offset exactly
-        shi -= 32 * s16(a.xs[jl + 2], L.hsel);
+        int slo = dot4((int)lo6[0], a.lo.x, 0);
+        slo = dot4((int)lo6[1], a.lo.y, slo);
+        slo = dot4((int)lo6[2], a.lo.z, slo);
+        slo = dot4((int)lo6[3], a.lo.w, slo);
+        int shi = dot4((int)hi6[0], a.hi.x, 0);
+        shi = dot4((int)hi6[1], a.hi.y, shi);
+        shi = dot4((int)hi6[2], a.hi.z, shi);
+        shi = dot4((int)hi6[3], a.hi.w, shi);
+        slo -= a.olo;
+        shi -= a.ohi;
         const int sclo = (int)(int8_t)(f.sc.x >> (8 * L.cc));
         const int schi = (int)(int8_t)(f.sc.y >> (8 * L.cc));
-        const float t = a.xd[jl] * ((float)slo * (float)sclo) + a.xd[jl + 2] * ((float)shi * (float)schi);
+        // |sums| <= 32 * 127 * 16 < 2^23 and |scales| <= 128: exact 24-bit products.
+        const float t = fmaf(a.dhi, (float)__mul24(shi, schi), a.dlo * (float)__mul24(slo, sclo));
         return f16_bits_to_f32(f.d) * t;
+    }
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        return dot(f, load_act(a, u, L), L);
     }
 
     __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
@@ -273,13 +326,25 @@ struct Q80 {
 
     __device__ static uint32_t stage_aux(float, uint32_t) { return 0u; }
 
+    struct AFrag {
+        int4 x;
+        float d;
+    };
+
+    __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
+        return {*(const int4 *)(a.xc + 128 * u + 32 * L.k + 16 * L.hf), a.xd[4 * u + L.k]};
+    }
+
+    // d_w dx sum(q q8) per block (vec_dot_q8_0_q8_1, exec:535-580), this lane's half.
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &) {
+        int s = dot4((int)f.q.x, a.x.x, 0);
+        s = dot4((int)f.q.y, a.x.y, s);
+        s = dot4((int)f.q.z, a.x.z, s);
+        s = dot4((int)f.q.w, a.x.w, s);
+        return f16_bits_to_f32(f.d) * (a.d * (float)s);
+    }
     __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
-        const int4 x = *(const int4 *)(a.xc + 128 * u + 32 * L.k + 16 * L.hf);
-        int s = dot4((int)f.q.x, x.x, 0);
-        s = dot4((int)f.q.y, x.y, s);
-        s = dot4((int)f.q.z, x.z, s);
-        s = dot4((int)f.q.w, x.w, s);
-        return f16_bits_to_f32(f.d) * (a.xd[4 * u + L.k] * (float)s);
+        return dot(f, load_act(a, u, L), L);
     }
 
     __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {

@@ -51,9 +51,11 @@ _SIGS = {
     "m27q_quant_act_gated": (_I, [_P, _P, _I, _I, _P, _P]),
     "m27q_matvec_q8": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P, _P]),
     "m27q_matvec_q8_multi": (_I, [_I, C.POINTER(WeightDesc), _P, C.POINTER(_P), _P]),
+    "m27q_matvec_multi": (_I, [_I, C.POINTER(WeightDesc), _P, C.POINTER(_P), _P]),
     "m27q_ffn_swiglu": (_I, [C.POINTER(WeightDesc), C.POINTER(WeightDesc), _P, _P, _P, _P]),
+    "m27q_ffn_swiglu_q8": (_I, [C.POINTER(WeightDesc), C.POINTER(WeightDesc), _P, _P, _P, _P]),
     "m27q_matvec_f32": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P]),
-    "m27q_matvec": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P, _SZ, _P]),
+    "m27q_matvec": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P, _P]),
     "m27q_matmul_q8": (_I, [C.POINTER(WeightDesc), _I, _P, _P, _P, _P]),
     "m27q_dequant_rows": (_I, [C.POINTER(WeightDesc), _I, _I, _P, _P]),
     "m27q_embed_rows": (_I, [C.POINTER(WeightDesc), _P, _I, _P, _P, _P]),
@@ -207,9 +209,24 @@ def matvec_q8_multi(ws: list[Weight], act: Act, ys: list, stream=None) -> None:
     check(lib().m27q_matvec_q8_multi(n, descs, _ptr(act.buf), yp, _stream(stream)), "m27q_matvec_q8_multi")
 
 
-def ffn_swiglu(gate: Weight, up: Weight, act: Act, y, yq: Act | None = None, stream=None) -> None:
+def matvec_multi(ws: list[Weight], x, ys: list, stream=None) -> None:
+    """fp32 activation x shared by up to 4 weights (quantized inside the kernel)."""
+    n = len(ws)
+    descs = (WeightDesc * n)(*[w.desc() for w in ws])
+    yp = (C.c_void_p * n)(*[_ptr(y) for y in ys])
+    check(lib().m27q_matvec_multi(n, descs, _ptr(x), yp, _stream(stream)), "m27q_matvec_multi")
+
+
+def ffn_swiglu_q8(gate: Weight, up: Weight, act: Act, y, yq: Act | None = None, stream=None) -> None:
     g, u = gate.desc(), up.desc()
-    check(lib().m27q_ffn_swiglu(C.byref(g), C.byref(u), _ptr(act.buf), _ptr(y),
+    check(lib().m27q_ffn_swiglu_q8(C.byref(g), C.byref(u), _ptr(act.buf), _ptr(y),
+                                   None if yq is None else _ptr(yq.buf), _stream(stream)), "m27q_ffn_swiglu_q8")
+
+
+def ffn_swiglu(gate: Weight, up: Weight, x, y, yq: Act | None = None, stream=None) -> None:
+    """fp32 activation x (quantized inside the kernel)."""
+    g, u = gate.desc(), up.desc()
+    check(lib().m27q_ffn_swiglu(C.byref(g), C.byref(u), _ptr(x), _ptr(y),
                                 None if yq is None else _ptr(yq.buf), _stream(stream)), "m27q_ffn_swiglu")
 
 
@@ -218,11 +235,11 @@ def matvec_f32(w: Weight, x, y, residual=None, stream=None) -> None:
     check(lib().m27q_matvec_f32(C.byref(d), _ptr(x), _ptr(y), _ptr(residual), _stream(stream)), "m27q_matvec_f32")
 
 
-def matvec(w: Weight, x, y, scratch, residual=None, stream=None) -> None:
+def matvec(w: Weight, x, y, residual=None, yq: Act | None = None, stream=None) -> None:
+    """fp32 activation x (quantized inside the kernel); F16/F32 weights take the fp32 path."""
     d = w.desc()
-    check(lib().m27q_matvec(C.byref(d), _ptr(x), _ptr(y), _ptr(residual), _ptr(scratch),
-                            0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream)),
-          "m27q_matvec")
+    check(lib().m27q_matvec(C.byref(d), _ptr(x), _ptr(y), _ptr(residual), None if yq is None else _ptr(yq.buf),
+                            _stream(stream)), "m27q_matvec")
 
 
 def matmul_q8(w: Weight, act: Act, Y, residual=None, stream=None) -> None:

@@ -294,9 +294,13 @@ void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k) {
 
 /* ------------------------------------------------ activation quantizer -- */
 
-/* One 32-value group.  The reference (exec:84-107) uses d = amax/127 and
- * q = roundf(x/d) under fast-math with no clamp; this path fixes the rule as
- * IEEE x/d, round half away from zero (roundf), clamp to +-127, fp32 d. */
+/* One 32-value group.  The reference's GPU kernel (exec:84-107) computes
+ * d = amax/127 and q = roundf(x/d) under --use_fast_math, where the divide
+ * becomes a multiply by an approximate reciprocal; that is not a pinnable
+ * IEEE rule.  This path fixes the rule of ggml's reference quantizer
+ * quantize_row_q8_1_ref: d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0
+ * (IEEE divide), q = roundf(x * id) (one fp32 multiply, round half away from
+ * zero), clamped to +-127, fp32 d. */
 static void quant_group32(const float *x, int8_t *q, float *d, uint32_t *s) {
     float amax = 0.f;
     for (int l = 0; l < 32; ++l) {
@@ -304,10 +308,11 @@ static void quant_group32(const float *x, int8_t *q, float *d, uint32_t *s) {
         if (a > amax) amax = a;
     }
     const float dd = amax / 127.f;
+    const float id = dd != 0.f ? 1.0f / dd : 0.f;
     int lo = 0, hi = 0;
     for (int l = 0; l < 32; ++l) {
-        int v = 0;
-        if (amax != 0.f) v = clampi((int)roundf(x[l] / dd), -127, 127);
+        const float t = x[l] * id;
+        const int v = clampi((int)roundf(t), -127, 127);
         q[l] = (int8_t)v;
         if (l < 16) lo += v; else hi += v;
     }

@@ -25,8 +25,10 @@
  *                         (ora_ref_vec_dot_q6_K_q8_1, exec:586-628) with one-hot
  *                         activations, plus single-bit known answers.
  *   ora_dequant_row_q8_0  the reference's dp4a formulation (exec:535-580).
- *   ora_quant_act         closed-form properties (|q|<=127, the max maps to +-127,
- *                         |x - d q| <= d/2, round-half-away on constructed ties).
+ *   ora_quant_act         an independent numpy restatement of the rule (float32
+ *                         divide / reciprocal / multiply, round half away in float64),
+ *                         and closed-form properties (|q|<=127, the max maps to +-127,
+ *                         |x - d q| <= d/2 (1 + 2^-22), round-half-away on ties).
  *   ora_dot_act           brute force (dequantized weights x dequantized activation
  *                         in fp64) on small shapes, and one-hot / zero inputs.
  *   ora_topk              numpy lexsort on the same values.
@@ -80,8 +82,9 @@ void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k);
 
 /* Activation format of the MI355X path: per 32 values, int8 codes, an fp32
- * scale d = amax/127 (IEEE divide), q = roundf(x/d) clamped to +-127, and the
- * two 16-value integer code sums packed as (int16 lo) | (int16 hi) << 16. */
+ * scale d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0 (IEEE divide),
+ * q = roundf(x * id) clamped to +-127 (ggml's quantize_row_q8_1_ref rule), and
+ * the two 16-value integer code sums packed as (int16 lo) | (int16 hi) << 16. */
 void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s);
 /* Same on x * sigmoid(g) (exec:109-138); sigmoid as 1/(1+expf(-g)). */
 void ora_quant_act_gated(const float *x, const float *g, int64_t k, int8_t *q, float *d, uint32_t *s);

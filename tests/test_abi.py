@@ -131,10 +131,19 @@ def test_validation_multi_and_swiglu(m27q):
     ys0 = (C.c_void_p * 2)(FAKE, None)
     ws3 = (m27q.WeightDesc * 2)(W(m27q), W(m27q))
     assert L.m27q_matvec_q8_multi(2, ws3, FAKE, ys0, None) == 1
-    g, u = W(m27q), W(m27q, rc=32)
-    assert L.m27q_ffn_swiglu(C.byref(g), C.byref(u), FAKE, FAKE, None, None) == 2
-    u = W(m27q, layout=m27q.GGUF)
-    assert L.m27q_ffn_swiglu(C.byref(g), C.byref(u), FAKE, FAKE, None, None) == 4
+    assert L.m27q_matvec_multi(2, ws, FAKE, ys, None) == 2
+    assert L.m27q_matvec_multi(2, ws3, None, ys, None) == 1
+    assert L.m27q_matvec_multi(2, ws3, FAKE + 4, ys, None) == 4          # fp32 x: 16-byte aligned
+    for fn in (L.m27q_ffn_swiglu, L.m27q_ffn_swiglu_q8):
+        g, u = W(m27q), W(m27q, rc=32)
+        assert fn(C.byref(g), C.byref(u), FAKE, FAKE, None, None) == 2
+        u = W(m27q, layout=m27q.GGUF)
+        assert fn(C.byref(g), C.byref(u), FAKE, FAKE, None, None) == 4
+        u = W(m27q, t=m27q.Q6_K)
+        assert fn(C.byref(g), C.byref(u), FAKE, FAKE, None, None) == 3
+        assert fn(C.byref(g), None, FAKE, FAKE, None, None) == 1
+        assert fn(C.byref(g), C.byref(g), None, FAKE, None, None) == 1
+        assert fn(C.byref(W(m27q, rc=40)), C.byref(W(m27q, rc=40)), FAKE, FAKE, FAKE, None) == 2
 
 
 def test_validation_activation_and_scratch(m27q):
@@ -145,8 +154,11 @@ def test_validation_activation_and_scratch(m27q):
     assert L.m27q_quant_act(FAKE, 1, 64, FAKE + 8, None) == 4
     assert L.m27q_quant_act_gated(FAKE, None, 1, 64, FAKE, None) == 1
     w = W(m27q)
-    assert L.m27q_matvec(C.byref(w), FAKE, FAKE, None, FAKE, 16, None) == 5
-    assert L.m27q_matvec(C.byref(w), FAKE, FAKE, None, None, 1 << 20, None) == 1
+    assert L.m27q_matvec(C.byref(w), None, FAKE, None, None, None) == 1
+    assert L.m27q_matvec(C.byref(w), FAKE, None, None, None, None) == 1
+    assert L.m27q_matvec(C.byref(W(m27q, rc=40)), FAKE, FAKE, None, FAKE, None) == 2
+    f16 = W(m27q, t=m27q.F16, rb=5120, layout=m27q.GGUF)
+    assert L.m27q_matvec(C.byref(f16), FAKE, FAKE, None, FAKE, None) == 3   # no fused quant on fp32 paths
     assert L.m27q_matmul_q8(C.byref(w), 0, FAKE, FAKE, None, None) == 2
     assert L.m27q_matmul_q8(C.byref(w), 65, FAKE, FAKE, None, None) == 2
 

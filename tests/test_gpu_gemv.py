@@ -151,7 +151,7 @@ def test_ffn_swiglu(m27q, ora, dev, type_name):
     g = torch.empty(rc, dtype=torch.float32, device=dev)
     u = torch.empty(rc, dtype=torch.float32, device=dev)
     say("swiglu", type_name)
-    m27q.ffn_swiglu(gw, uw, act, y, yq=yq)
+    m27q.ffn_swiglu_q8(gw, uw, act, y, yq=yq)
     m27q.matvec_q8(gw, act, g)
     m27q.matvec_q8(uw, act, u)
     gh, uh, yh = to_host(g).astype(np.float64), to_host(u).astype(np.float64), to_host(y).astype(np.float64)
@@ -204,22 +204,55 @@ def test_matvec_dense(m27q, ora, dev, type_name):
     assert (np.abs(to_host(y) - want) <= 1e-5 * scale).all()
 
 
-def test_matvec_with_scratch_equals_two_step(m27q, ora, dev):
+@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 6144, 5120), ("Q8_0", 13, 160)])
+def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
+    """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so the
+    product is bit-identical to quant_act followed by the quantized-input product."""
     import torch
-    rc, k = 5120, 17408
-    wb = weights(ora, "Q6_K", rc, k, 10)
-    w = m27q.Weight.upload(wb.reshape(-1), m27q.Q6_K, 68, rc, m27q.TILED, dev)
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
     x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
     xd = to_dev(x, dev)
-    scratch = torch.empty(m27q.act_bytes(1, k), dtype=torch.uint8, device=dev)
+    res = to_dev(np.random.default_rng(2).standard_normal(rc).astype(np.float32), dev)
     y0 = torch.empty(rc, dtype=torch.float32, device=dev)
     y1 = torch.empty(rc, dtype=torch.float32, device=dev)
-    say("matvec with scratch")
-    m27q.matvec(w, xd, y0, scratch)
+    say("matvec fp32 input", type_name)
+    m27q.matvec(w, xd, y0, residual=res)
     act = m27q.Act(1, k, dev)
     m27q.quant_act(xd, act)
-    m27q.matvec_q8(w, act, y1)
+    m27q.matvec_q8(w, act, y1, residual=res)
     assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
+
+
+def test_fp32_input_multi_and_swiglu(m27q, ora, dev):
+    import torch
+    k = 5120
+    shapes = [6144, 1024, 1024]
+    ws = [m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 40 + i).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
+          for i, rc in enumerate(shapes)]
+    x = to_dev(np.random.default_rng(11).standard_normal(k).astype(np.float32), dev)
+    act = m27q.Act(1, k, dev)
+    m27q.quant_act(x, act)
+    ya = [torch.empty(rc, dtype=torch.float32, device=dev) for rc in shapes]
+    yb = [torch.empty(rc, dtype=torch.float32, device=dev) for rc in shapes]
+    say("multi fp32 input")
+    m27q.matvec_multi(ws, x, ya)
+    m27q.matvec_q8_multi(ws, act, yb)
+    for a, b in zip(ya, yb):
+        assert np.array_equal(to_host(a).view(np.uint32), to_host(b).view(np.uint32))
+    rc = 17408
+    gw = m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 30).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
+    uw = m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 31).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
+    y0 = torch.empty(rc, dtype=torch.float32, device=dev)
+    y1 = torch.empty(rc, dtype=torch.float32, device=dev)
+    q0, q1 = m27q.Act(1, rc, dev), m27q.Act(1, rc, dev)
+    say("swiglu fp32 input")
+    m27q.ffn_swiglu(gw, uw, x, y0, yq=q0)
+    m27q.ffn_swiglu_q8(gw, uw, act, y1, yq=q1)
+    assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
+    assert np.array_equal(to_host(q0.buf), to_host(q1.buf))
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 17408, 5120), ("Q6_K", 5120, 17408)])

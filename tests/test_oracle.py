@@ -153,12 +153,32 @@ def test_quant_act_properties(ora):
     assert (np.abs(qg) <= 127).all()
     assert (np.abs(qg).max(-1) == 127).all()
     err = np.abs(g.astype(np.float64) - qg * d[..., None].astype(np.float64))
-    assert (err <= 0.5 * d[..., None] * (1 + 1e-6)).all()
+    assert (err <= 0.5 * d[..., None] * (1 + 2.0 ** -22) + 1e-45).all()
     lo = qg[..., :16].sum(-1)
     hi = qg[..., 16:].sum(-1)
     s = s.astype(np.int64)
     assert np.array_equal(((s & 0xFFFF) ^ 0x8000) - 0x8000, lo)
     assert np.array_equal(((s >> 16) ^ 0x8000) - 0x8000, hi)
+
+
+def test_quant_act_matches_numpy_restatement(ora):
+    """The documented rule restated in numpy: float32 d = amax / 127, id = 1 / d
+    (0 when d == 0), t = float32(x * id), code = round half away from zero of t
+    (evaluated exactly in float64), clamped to +-127."""
+    x = (RNG.standard_normal((8, 2048)) * 10.0 ** RNG.integers(-8, 8, (8, 1))).astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, 32:64] = np.float32(1e-44)  # d underflows to 0: every code 0
+    q, d, s = ora.quant_act(x)
+    g = x.reshape(8, -1, 32)
+    amax = np.abs(g).max(-1)
+    dd = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(dd != 0, np.float32(1) / dd, np.float32(0)).astype(np.float32)
+    t = (g * idv[..., None]).astype(np.float32).astype(np.float64)
+    want = np.clip(np.sign(t) * np.floor(np.abs(t) + 0.5), -127, 127).astype(np.int64)
+    assert np.array_equal(d, dd)
+    assert np.array_equal(q.reshape(8, -1, 32).astype(np.int64), want)
+    assert (q[0, :32] == 0).all() and (q[1, 32:64] == 0).all()
 
 
 def test_quant_act_rounds_half_away_from_zero(ora):
