@@ -106,6 +106,19 @@ def stage_bytes(m27q, name):
     return wb + (k + 8 * (k // 32)) + 4 * n + 4 * n      # quantized input, + residual
 
 
+def measured_traffic(kernel_label):
+    """HBM bytes per launch of one product as measured by rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE, scaled by a kernel of known size), read from
+    the committed summary; None where that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_decode_layer_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(kernel_label + ":"):
+            return int(line.split()[-3])
+    return None
+
+
 def layer_pass(m27q, L, B, stream):
     for fn in STAGES.values():
         fn(m27q, L, B, stream)
@@ -167,6 +180,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: auto, >= 2x MALL)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run a plain 512 MiB device copy (the reference point that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build is single-GPU by design); got --gpus {args.gpus}",
@@ -215,6 +231,26 @@ def main():
         log(f"{name}: {ms * 1e3:.2f} us, {stages[name]['GBps']} GB/s")
     dom = stages["gate_up"]  # the dominant product: 100 MB of the layer's 215 MB
 
+    # Plain streaming read of 1 GiB (torch's sum kernel) for the measured peak.
+    big = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    big.sum()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        big.sum()
+    e1.record()
+    e1.synchronize()
+    read_gbs = big.numel() * 4 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del big
+    if args.calib:
+        src = torch.ones(1 << 27, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     gbs = layer_bytes / (ms_cold * 1e-3) / 1e9
     rec = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
@@ -230,11 +266,13 @@ def main():
         "lower_bound_us": round(layer_bytes / HBM_PEAK_GBS / 1e3, 2),
         "x_lower_bound": round(ms_cold * 1e3 / (layer_bytes / HBM_PEAK_GBS / 1e3), 3),
         "warm_us_per_layer": round(ms_warm * 1e3, 2),
+        "hbm_read_GBps_measured": round(read_gbs, 1),
         "stages": stages,
         "roofline": {"bound": "hbm", "kernel": "k_gemv_q8<Q4K,TILED,SWIGLU> (gate+up 17408x5120, fp32 x in, "
                                                "fp32 + quantized out)",
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up"),
+                     "traffic_source": "profiles/gemv_decode_layer_hbm_traffic.txt",
                      "avg_launch_us": dom["us"], "algorithmic_bytes": dom["bytes"]},
     }
     if not args.no_cpu:
