@@ -106,11 +106,12 @@ M27Q_API m27q_status m27q_unpack(uint32_t ggml_type, uint32_t row_blocks, uint32
  *   int8  codes[M][K]             at offset 0
  *   float d[M][K/32]              at offset m27q_act_d_offset(M, K)
  *   u32   sums[M][K/32]           at offset m27q_act_s_offset(M, K)
- * Per 32 values: d = amax/127 (IEEE divide), code = roundf(x/d) clamped to
- * +-127 (0 when amax == 0), sums = (int16 sum of codes 0..15) |
- * (int16 sum of codes 16..31) << 16.  The reference's Q8_1 (exec:65-71) keeps
- * an fp16 d and the float sum of x; this format keeps an fp32 d and the exact
- * integer sums its dot products use. */
+ * Per 32 values: d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0 (IEEE
+ * divide), code = roundf(x * id) clamped to +-127 (the rule of ggml's
+ * quantize_row_q8_1_ref), sums = (int16 sum of codes 0..15) | (int16 sum of
+ * codes 16..31) << 16.  The reference's Q8_1 (exec:65-71) keeps an fp16 d and
+ * the float sum of x; this format keeps an fp32 d and the exact integer sums
+ * its dot products use. */
 M27Q_API size_t m27q_act_bytes(int M, int K);
 M27Q_API size_t m27q_act_d_offset(int M, int K);
 M27Q_API size_t m27q_act_s_offset(int M, int K);

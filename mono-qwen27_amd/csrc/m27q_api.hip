@@ -74,14 +74,6 @@ int wg_count(int rows) { return ((rows + kTileRows - 1) / kTileRows + kWavesPerW
 
 m27q_status hip_status(hipError_t e) { return e == hipSuccess ? M27Q_OK : M27Q_ERR_HIP; }
 
-// Launch configuration for a product of upr units per row (m27q_gemv_cfg.h).
-int pick_gemv_cfg(int upr, bool out_quant) {
-    if (out_quant) return kCfgOutQ;
-    if (upr >= 40) return kCfgLongK;
-    if (upr >= 25) return kCfgMidK;
-    return kCfgShortK;
-}
-
 m27q_status check_out_quant(const m27q_weight *w, const void *yq) {
     if (!yq) return M27Q_OK;
     if (!aligned(yq, 16)) return M27Q_ERR_LAYOUT;
@@ -118,7 +110,10 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     p.rb = (int)ws[0].row_blocks;
     p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
     p.K = k_of(&ws[0]);
-    const int cfg = pick_gemv_cfg(p.upr, yq != nullptr);
+    long long rows_total = 0;
+    for (int i = 0; i < n; ++i) rows_total += ws[i].row_count;
+    if (swiglu) rows_total = ws[0].row_count;
+    const int cfg = pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq != nullptr, rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
     if (x) {
         p.x = x;

@@ -165,15 +165,38 @@ __device__ __forceinline__ void compute_unit(const typename T::Frag (&f)[NM][TPW
         for (int t = 0; t < TPW; ++t) acc[m][t] += T::dot(f[m][t], a, L);
 }
 
+// Fused per-32 quantization of the output rows: the workgroup's NR rows are
+// whole 32-row groups (rc % 32 == 0 and NR % 32 == 0 are checked on the host).
+// Sharing a group between workgroups would need a device-scope fence, which
+// on a multi-XCD part writes back the whole L2 of the XCD (measured: 20x
+// slower), so output-quantizing products always launch 32-row workgroups.
+template <int NR>
+__device__ __forceinline__ void quant_output(const GemvParams &p, int row0, int rc, float v) {
+    static_assert(NR % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
+    const int t = (int)threadIdx.x;
+    if (t < NR && row0 + (t & ~31) < rc) {
+        const int row = row0 + t;
+        float d;
+        uint32_t s;
+        const int q = quant32(v, &d, &s);
+        p.oq[row] = (int8_t)q;
+        if ((t & 31) == 0) {
+            p.od[row / 32] = d;
+            p.os[row / 32] = s;
+        }
+    }
+}
+
 template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>
-__global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
+__global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int KS = C::KS, TPW = C::TPW;
+    constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int NR = TPW * kTileRows;  // rows per workgroup
     const int lane = (int)(threadIdx.x & 63), i = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int nth = KS * kWave;
+    const int ks = wave % KS, tg = wave / KS;  // K slice and tile group of this wave
+    const int nth = C::NW * kWave;
 
     // Matrix of this workgroup (up to kMaxMulti matrices share one launch).
     int m = 0;
@@ -187,8 +210,8 @@ __global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
     // K slice of this wave: units [ub, ub + nu); a wave with no units reads a
     // valid unit and discards it.
     const int U = p.upr / KS, rem = p.upr % KS;
-    const int ub = wave * U + min(wave, rem);
-    const int nu = U + (wave < rem ? 1 : 0);
+    const int ub = ks * U + min(ks, rem);
+    const int nu = U + (ks < rem ? 1 : 0);
 
     // 1. first batch of the activation, 2. the first unit of weights (their
     // latency overlaps the staging), 3. activation to LDS.
@@ -199,8 +222,8 @@ __global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
     const uint8_t *W[NM];
     W[0] = p.W[m];
     if constexpr (SWIGLU) W[NM - 1] = p.W[1];
-    const UnitStream<T, LAYOUT, NM, TPW> ws(W, tile0, ntiles, rc, p.rb, p.upr, lane);
-    typename T::Frag fa[NM][TPW], fb[NM][TPW];
+    const UnitStream<T, LAYOUT, NM, WT> ws(W, tile0 + tg * WT, ntiles, rc, p.rb, p.upr, lane);
+    typename T::Frag fa[NM][WT], fb[NM][WT];
     ws.load(fa, min(ub, p.upr - 1));
 
     stage_store<T, XF32>(sr, smem, Kp, (int)threadIdx.x, nth);
@@ -212,41 +235,42 @@ __global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
     float *red = (float *)(smem + Kp + Kp / 4);  // [NM][KS][NR]
     __syncthreads();
 
-    float acc[NM][TPW];
+    float acc[NM][WT];
 #pragma unroll
     for (int mm = 0; mm < NM; ++mm)
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) acc[mm][t] = 0.f;
+        for (int t = 0; t < WT; ++t) acc[mm][t] = 0.f;
     int k = 0;
     for (; k + 2 < nu; k += 2) {
         ws.load(fb, ub + k + 1);
-        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
+        compute_unit<T, NM, WT>(fa, act, ub + k, ws.L, acc);
         ws.load(fa, ub + k + 2);
-        compute_unit<T, NM, TPW>(fb, act, ub + k + 1, ws.L, acc);
+        compute_unit<T, NM, WT>(fb, act, ub + k + 1, ws.L, acc);
     }
     if (k + 1 < nu) {
         ws.load(fb, ub + k + 1);
-        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
-        compute_unit<T, NM, TPW>(fb, act, ub + k + 1, ws.L, acc);
+        compute_unit<T, NM, WT>(fa, act, ub + k, ws.L, acc);
+        compute_unit<T, NM, WT>(fb, act, ub + k + 1, ws.L, acc);
     } else if (k < nu) {
-        compute_unit<T, NM, TPW>(fa, act, ub + k, ws.L, acc);
+        compute_unit<T, NM, WT>(fa, act, ub + k, ws.L, acc);
     }
 
     // Row partials of this wave's slice -> LDS.
 #pragma unroll
     for (int mm = 0; mm < NM; ++mm)
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) {
+        for (int t = 0; t < WT; ++t) {
             const float r = sum8(acc[mm][t]);
-            if (c == 0) red[(mm * KS + wave) * NR + t * kTileRows + i] = r;
+            if (c == 0) red[(mm * KS + ks) * NR + (tg * WT + t) * kTileRows + i] = r;
         }
     __syncthreads();
 
     // Epilogue: one thread per row of the workgroup.
     const int t = (int)threadIdx.x;
+    float v = 0.f;
     if (t < NR) {
         const int row = tile0 * kTileRows + t;
-        float v = red[t];
+        v = red[t];
 #pragma unroll
         for (int w = 1; w < KS; ++w) v += red[w * NR + t];
         if constexpr (SWIGLU) {
@@ -258,19 +282,9 @@ __global__ __launch_bounds__(kWave *C::KS) void k_gemv_q8(GemvParams p) {
             if (p.res[m] && row < rc) v += p.res[m][row];
         }
         if (row < rc) p.y[m][row] = v;
-        // Fused per-32 quantization of the output (rc % 32 == 0 and NR % 32 == 0
-        // are checked on the host, so a 32-row group is wholly in or out).
-        if (p.oq && tile0 * kTileRows + (t & ~31) < rc) {
-            float d;
-            uint32_t s;
-            const int q = quant32(v, &d, &s);
-            p.oq[row] = (int8_t)q;
-            if ((t & 31) == 0) {
-                p.od[row / 32] = d;
-                p.os[row / 32] = s;
-            }
-        }
     }
+    if constexpr (NR % 32 == 0)
+        if (p.oq) quant_output<NR>(p, tile0 * kTileRows, rc, v);
 }
 
 // ------------------------------------------------ fp32-activation products --
@@ -394,18 +408,22 @@ size_t gemv_q8_lds(int upr) {
 template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>
 static hipError_t launch_q8_cfg(const GemvParams &p, hipStream_t s) {
     const size_t lds = gemv_q8_lds<T, C, SWIGLU>(p.upr);
-    hipLaunchKernelGGL((k_gemv_q8<T, LAYOUT, C, SWIGLU, XF32>), dim3(p.wg_start[p.nmat]), dim3(kWave * C::KS), lds, s,
+    hipLaunchKernelGGL((k_gemv_q8<T, LAYOUT, C, SWIGLU, XF32>), dim3(p.wg_start[p.nmat]), dim3(kWave * C::NW), lds, s,
                        p);
     return hipGetLastError();
 }
 
 template <class T, int LAYOUT, bool SWIGLU, bool XF32>
 static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
+    if constexpr (LAYOUT == M27Q_LAYOUT_GGUF)
+        return cfg == kCfgQ ? launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s)
+                            : launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     switch (cfg) {
-        case kCfgLongK: return launch_q8_cfg<T, LAYOUT, CfgLongK, SWIGLU, XF32>(p, s);
-        case kCfgMidK: return launch_q8_cfg<T, LAYOUT, CfgMidK, SWIGLU, XF32>(p, s);
-        case kCfgOutQ: return launch_q8_cfg<T, LAYOUT, CfgOutQ, SWIGLU, XF32>(p, s);
-        default: return launch_q8_cfg<T, LAYOUT, CfgShortK, SWIGLU, XF32>(p, s);
+        case kCfgQ: return launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s);
+        case kCfg81: return launch_q8_cfg<T, LAYOUT, Cfg81, SWIGLU, XF32>(p, s);
+        case kCfg42: return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
+        case kCfg84: return launch_q8_cfg<T, LAYOUT, Cfg84, SWIGLU, XF32>(p, s);
+        default: return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     }
 }
 
@@ -422,13 +440,19 @@ static hipError_t launch_q8_x(const GemvParams &p, int layout, bool swiglu, int 
     return xf ? launch_q8_l<T, false, true>(p, layout, cfg, s) : launch_q8_l<T, false, false>(p, layout, cfg, s);
 }
 
+template <class T, class C>
+static size_t lds_sw(int upr, bool swiglu) {
+    return swiglu ? gemv_q8_lds<T, C, true>(upr) : gemv_q8_lds<T, C, false>(upr);
+}
+
 template <class T>
 static size_t lds_for(int upr, bool swiglu, int cfg) {
     switch (cfg) {
-        case kCfgLongK: return swiglu ? gemv_q8_lds<T, CfgLongK, true>(upr) : gemv_q8_lds<T, CfgLongK, false>(upr);
-        case kCfgMidK: return swiglu ? gemv_q8_lds<T, CfgMidK, true>(upr) : gemv_q8_lds<T, CfgMidK, false>(upr);
-        case kCfgOutQ: return swiglu ? gemv_q8_lds<T, CfgOutQ, true>(upr) : gemv_q8_lds<T, CfgOutQ, false>(upr);
-        default: return swiglu ? gemv_q8_lds<T, CfgShortK, true>(upr) : gemv_q8_lds<T, CfgShortK, false>(upr);
+        case kCfg81: return lds_sw<T, Cfg81>(upr, swiglu);
+        case kCfg42: return lds_sw<T, Cfg42>(upr, swiglu);
+        case kCfg84: return lds_sw<T, Cfg84>(upr, swiglu);
+        case kCfgQ: return lds_sw<T, CfgQ>(upr, swiglu);
+        default: return lds_sw<T, Cfg41>(upr, swiglu);
     }
 }
 
@@ -443,10 +467,11 @@ size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg) {
 
 int gemv_q8_tiles_per_wg(int cfg) {
     switch (cfg) {
-        case kCfgLongK: return CfgLongK::TPW;
-        case kCfgMidK: return CfgMidK::TPW;
-        case kCfgOutQ: return CfgOutQ::TPW;
-        default: return CfgShortK::TPW;
+        case kCfg81: return Cfg81::TPW;
+        case kCfg42: return Cfg42::TPW;
+        case kCfg84: return Cfg84::TPW;
+        case kCfgQ: return CfgQ::TPW;
+        default: return Cfg41::TPW;
     }
 }
 

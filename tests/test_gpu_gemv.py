@@ -117,6 +117,30 @@ def test_fused_output_quant_matches_standalone(m27q, ora, dev):
     assert np.array_equal(act_host(m27q, yq)[0][0], qo)
 
 
+@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 17408, 5120), ("Q4_K", 5120, 6144), ("Q8_0", 2048, 6144),
+                                             ("Q6_K", 5120, 17408), ("Q4_K", 1024, 5120)])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_fused_output_quant_shapes(m27q, ora, dev, type_name, rc, k, layout):
+    """The fused output quantization at every workgroup shape the products pick
+    for these sizes; two calls in a row on one buffer both match the standalone
+    quantizer."""
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 14)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, layout, dev)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    yq = m27q.Act(1, rc, dev)
+    ref = m27q.Act(1, rc, dev)
+    for call in range(2):
+        x = to_dev(np.random.default_rng(50 + call).standard_normal(k).astype(np.float32), dev)
+        say("fused output quant", type_name, rc, k, "call", call)
+        m27q.matvec(w, x, y, yq=yq)
+        m27q.quant_act(y, ref)
+        for a, b in zip(act_host(m27q, yq), act_host(m27q, ref)):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), call
+
+
 def test_multi_matches_single(m27q, ora, dev):
     import torch
     k = 5120
@@ -152,18 +176,25 @@ def test_ffn_swiglu(m27q, ora, dev, type_name):
     u = torch.empty(rc, dtype=torch.float32, device=dev)
     say("swiglu", type_name)
     m27q.ffn_swiglu_q8(gw, uw, act, y, yq=yq)
-    m27q.matvec_q8(gw, act, g)
-    m27q.matvec_q8(uw, act, u)
-    gh, uh, yh = to_host(g).astype(np.float64), to_host(u).astype(np.float64), to_host(y).astype(np.float64)
-    silu = gh / (1 + np.exp(-gh))
-    assert np.allclose(yh, silu * uh, rtol=2e-6, atol=1e-7 * np.abs(silu * uh).max())
     q, d, s = act_host(m27q, act)
-    want_g, ng = ora.gemv_act(t, gb, 20, rc, q[0], d[0], s[0])
-    assert (np.abs(gh - want_g) <= int_dot_tol(ng)).all()
+    check_swiglu(ora, t, gb, ub, rc, q[0], d[0], s[0], to_host(y))
     ref = m27q.Act(1, rc, dev)
     m27q.quant_act(y, ref)
     for a, b in zip(act_host(m27q, yq), act_host(m27q, ref)):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def check_swiglu(ora, t, gb, ub, rc, q, d, s, y):
+    """y = silu(g) u against the fp64 integer-dot oracle: the fp32 error of g and
+    u (int_dot_tol each) propagated through silu(g) u (|silu'| < 1.1), plus the
+    rounding of the epilogue itself."""
+    g, ng = ora.gemv_act(t, gb, 20, rc, q, d, s)
+    u, nu = ora.gemv_act(t, ub, 20, rc, q, d, s)
+    sg = g / (1 + np.exp(-g))
+    want = sg * u
+    tol = 1.1 * np.abs(u) * int_dot_tol(ng) + np.abs(sg) * int_dot_tol(nu) + 4e-7 * np.abs(want) + 1e-30
+    err = np.abs(y.astype(np.float64) - want)
+    assert (err <= tol).all(), (np.flatnonzero(err > tol)[:5], err.max())
 
 
 @pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged"])
@@ -204,10 +235,12 @@ def test_matvec_dense(m27q, ora, dev, type_name):
     assert (np.abs(to_host(y) - want) <= 1e-5 * scale).all()
 
 
-@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 6144, 5120), ("Q8_0", 13, 160)])
+@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 5120, 6144), ("Q4_K", 17408, 5120),
+                                             ("Q8_0", 2048, 6144)])
 def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
-    """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so the
-    product is bit-identical to quant_act followed by the quantized-input product."""
+    """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so at
+    shapes where both input forms launch the same workgroup shape the product
+    is bit-identical to quant_act followed by the quantized-input product."""
     import torch
     t = getattr(m27q, type_name)
     rb = k // m27q.BLOCK_ELEMS[t]
@@ -226,33 +259,50 @@ def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
 
 
+@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 6144, 5120), ("Q8_0", 13, 160), ("Q4_K", 40, 512)])
+def test_fp32_input_vs_oracle(m27q, ora, dev, type_name, rc, k):
+    """Shapes where the fp32-input product launches its own workgroup shape:
+    against the integer-dot oracle on the codes of the standalone quantizer."""
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 10)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    x = np.random.default_rng(3).standard_normal(k).astype(np.float32)
+    y = torch.empty(rc, dtype=torch.float32, device=dev)
+    say("matvec fp32 input vs oracle", type_name, rc, k)
+    m27q.matvec(w, to_dev(x, dev), y)
+    q, d, s = ora.quant_act(x)
+    want, nrm = ora.gemv_act(t, wb, rb, rc, q, d, s)
+    assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
+
+
 def test_fp32_input_multi_and_swiglu(m27q, ora, dev):
     import torch
     k = 5120
     shapes = [6144, 1024, 1024]
-    ws = [m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 40 + i).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
-          for i, rc in enumerate(shapes)]
-    x = to_dev(np.random.default_rng(11).standard_normal(k).astype(np.float32), dev)
-    act = m27q.Act(1, k, dev)
-    m27q.quant_act(x, act)
+    wbs = [weights(ora, "Q4_K", rc, k, 40 + i) for i, rc in enumerate(shapes)]
+    ws = [m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev) for wb, rc in zip(wbs, shapes)]
+    xh = np.random.default_rng(11).standard_normal(k).astype(np.float32)
+    x = to_dev(xh, dev)
     ya = [torch.empty(rc, dtype=torch.float32, device=dev) for rc in shapes]
-    yb = [torch.empty(rc, dtype=torch.float32, device=dev) for rc in shapes]
     say("multi fp32 input")
     m27q.matvec_multi(ws, x, ya)
-    m27q.matvec_q8_multi(ws, act, yb)
-    for a, b in zip(ya, yb):
-        assert np.array_equal(to_host(a).view(np.uint32), to_host(b).view(np.uint32))
+    q, d, s = ora.quant_act(xh)
+    for wb, rc, y in zip(wbs, shapes, ya):
+        want, nrm = ora.gemv_act(m27q.Q4_K, wb, 20, rc, q, d, s)
+        assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
     rc = 17408
-    gw = m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 30).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
-    uw = m27q.Weight.upload(weights(ora, "Q4_K", rc, k, 31).reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
+    gb, ub = weights(ora, "Q4_K", rc, k, 30), weights(ora, "Q4_K", rc, k, 31)
+    gw = m27q.Weight.upload(gb.reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
+    uw = m27q.Weight.upload(ub.reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev)
     y0 = torch.empty(rc, dtype=torch.float32, device=dev)
-    y1 = torch.empty(rc, dtype=torch.float32, device=dev)
-    q0, q1 = m27q.Act(1, rc, dev), m27q.Act(1, rc, dev)
+    q0, ref = m27q.Act(1, rc, dev), m27q.Act(1, rc, dev)
     say("swiglu fp32 input")
     m27q.ffn_swiglu(gw, uw, x, y0, yq=q0)
-    m27q.ffn_swiglu_q8(gw, uw, act, y1, yq=q1)
-    assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
-    assert np.array_equal(to_host(q0.buf), to_host(q1.buf))
+    check_swiglu(ora, m27q.Q4_K, gb, ub, rc, q, d, s, to_host(y0))
+    m27q.quant_act(y0, ref)
+    assert np.array_equal(to_host(q0.buf), to_host(ref.buf))
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 17408, 5120), ("Q6_K", 5120, 17408)])
