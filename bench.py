@@ -119,6 +119,88 @@ def measured_traffic(kernel_label):
     return None
 
 
+def rand_weight(m27q, torch, dev, t, rc, k, layout=None):
+    """Random valid-size weight bytes (timing only; parity is the tests' job).
+    fp16 scales are forced finite."""
+    layout = m27q.TILED if layout is None else layout
+    rb = k // m27q.BLOCK_ELEMS[t]
+    raw = torch.randint(0, 256, (rc * rb, m27q.BLOCK_BYTES[t]), dtype=torch.uint8, device=dev)
+    if t == m27q.Q6_K:
+        raw[:, 209] = 0x0a
+    else:
+        raw[:, 1] = 0x0a
+        if t == m27q.Q4_K:
+            raw[:, 3] = 0x0a
+    if layout == m27q.GGUF:
+        return m27q.Weight(raw.reshape(-1), t, rb, rc, layout)
+    host = m27q.repack(t, rb, rc, raw.cpu().numpy().reshape(-1))
+    return m27q.Weight(torch.from_numpy(host).to(dev), t, rb, rc, layout)
+
+
+def timed(torch, fn, ncopies, reps):
+    """Average us per call of fn(c, stream) over ncopies rotated inputs, captured in a graph."""
+    g = capture(torch, lambda st: [fn(c, st) for c in range(ncopies)])
+    g.replay()
+    return time_graph(torch, g, reps) / ncopies * 1e3
+
+
+def suite(m27q, torch, dev, layers, reps):
+    """The other configurations of the path, each timed cold (rotated copies >= 2 x MALL)."""
+    out = {}
+    rng = np.random.default_rng(5)
+    x5120 = torch.from_numpy(rng.standard_normal(5120).astype(np.float32)).to(dev)
+    # config 1: Q4_K 17408 x 5120 alone, fp32 x
+    y = torch.empty(17408, dtype=torch.float32, device=dev)
+    us = timed(torch, lambda c, st: m27q.matvec(layers[c % len(layers)]["gate"], x5120, y, stream=st), len(layers), reps)
+    out["cfg1_q4k_17408x5120_m1"] = {"us": round(us, 3), "GBps": round(50135040 / us / 1e3, 1)}
+    log(f"config 1: {us:.2f} us")
+    # config 2: Q8_0 draft shapes, fp32 x
+    for rc, k in ((2048, 2048), (6144, 2048), (2048, 6144)):
+        nbytes = rc * k // 32 * 34
+        nc = max(2, -(-2 * MALL_BYTES // nbytes) + 1)
+        ws = [rand_weight(m27q, torch, dev, m27q.Q8_0, rc, k) for _ in range(nc)]
+        xx = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(dev)
+        yy = torch.empty(rc, dtype=torch.float32, device=dev)
+        us = timed(torch, lambda c, st: m27q.matvec(ws[c], xx, yy, stream=st), nc, reps)
+        out[f"cfg2_q80_{rc}x{k}_m1"] = {"us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)}
+        del ws
+    log("config 2 done")
+    # config 4: the layer's products on M quantized activation rows
+    for M in (2, 4, 8, 16):
+        acts = {k: m27q.Act(M, k, dev) for k in (5120, 6144, 17408)}
+        for k, a in acts.items():
+            m27q.quant_act(torch.from_numpy(rng.standard_normal((M, k)).astype(np.float32)).to(dev), a)
+        Ys = {n: torch.empty((M, rc), dtype=torch.float32, device=dev) for n, _, rc, _ in LAYER}
+
+        def layer_m(c, st):
+            L = layers[c]
+            m27q.matmul_q8_multi([L["q"], L["k"], L["v"]], acts[5120], [Ys["q"], Ys["k"], Ys["v"]], stream=st)
+            m27q.matmul_q8(L["o"], acts[6144], Ys["o"], stream=st)
+            m27q.matmul_q8_multi([L["gate"], L["up"]], acts[5120], [Ys["gate"], Ys["up"]], stream=st)
+            m27q.matmul_q8(L["down"], acts[17408], Ys["down"], stream=st)
+        us = timed(torch, layer_m, len(layers), reps)
+        lb = sum(m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256 for _, t, rc, k in LAYER)
+        out[f"cfg4_layer_m{M}"] = {"us": round(us, 3), "GBps": round(lb / us / 1e3, 1)}
+        log(f"config 4 M={M}: {us:.2f} us")
+    # config 5: LM head GEMV, exact top-64, 512-row gather
+    lm = rand_weight(m27q, torch, dev, m27q.Q6_K, 248320, 5120)
+    logits = torch.empty(248320, dtype=torch.float32, device=dev)
+    us = timed(torch, lambda c, st: m27q.matvec(lm, x5120, logits, stream=st), 1, max(2, reps // 4))
+    out["cfg5_lm_head_q6k_248320x5120"] = {"us": round(us, 3), "GBps": round(248320 * 4200 / us / 1e3, 1)}
+    k = 64
+    scratch = torch.empty(m27q.topk_scratch_bytes(248320, k), dtype=torch.uint8, device=dev)
+    idx = torch.empty(k, dtype=torch.int32, device=dev)
+    val = torch.empty(k, dtype=torch.float32, device=dev)
+    us = timed(torch, lambda c, st: m27q.topk(logits, k, idx, val, scratch, stream=st), 1, reps)
+    out["cfg5_topk64_of_248320"] = {"us": round(us, 3), "GBps": round(248320 * 4 / us / 1e3, 1)}
+    ids = torch.from_numpy(rng.integers(0, 248320, 512).astype(np.int32)).to(dev)
+    rows = torch.empty((512, 5120), dtype=torch.float32, device=dev)
+    us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids, rows, stream=st), 1, reps)
+    out["cfg5_gather_512_q6k_rows"] = {"us": round(us, 3), "GBps": round((512 * 4200 + 512 * 5120 * 4) / us / 1e3, 1)}
+    log("config 5 done")
+    return out
+
+
 def layer_pass(m27q, L, B, stream):
     for fn in STAGES.values():
         fn(m27q, L, B, stream)
@@ -180,6 +262,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: auto, >= 2x MALL)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-suite", action="store_true", help="skip the configurations other than the layer")
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain 512 MiB device copy (the reference point that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -275,6 +358,8 @@ def main():
                      "traffic_source": "profiles/gemv_decode_layer_hbm_traffic.txt",
                      "avg_launch_us": dom["us"], "algorithmic_bytes": dom["bytes"]},
     }
+    if not args.no_suite:
+        rec["suite"] = suite(m27q, torch, dev, layers, reps)
     if not args.no_cpu:
         log("cpu baseline")
         rec["cpu_baseline"] = cpu_baseline(ora, host)

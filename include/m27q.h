@@ -183,12 +183,20 @@ M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float
  * ---------------------------------------------------------------------- */
 
 /* Y[m][r] = sum_k W[r][k] * xq[m][k] (+ residual[m][r]) for m < M, 1 <= M <= 64,
- * xq from m27q_quant_act with this M.  Integer MFMA for M >= 16, packed int8 dot
- * below.  No reference counterpart: the reference runs prefill and decode one
- * token at a time (src/mono27b_chat.cpp:399-403); results equal M independent
- * M = 1 products. */
+ * xq from m27q_quant_act with this M; Y is [M][row_count].  TILED weights run
+ * on int8 MFMA (v_mfma_i32_16x16x32_i8, 16 activation rows per launch); GGUF
+ * weights on a packed-int8-dot path; M = 1 is m27q_matvec_q8.  No reference
+ * counterpart: the reference runs prefill and decode one token at a time
+ * (src/mono27b_chat.cpp:399-403); results equal M independent M = 1 products
+ * up to fp32 rounding. */
 M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y,
                                     const float *residual, hipStream_t stream);
+
+/* Up to 4 TILED weights of one type and K on the same M activation rows, in
+ * one launch: Ys[i] = X W[i]^T ([M][row_count_i] each).  The small-M
+ * counterpart of m27q_matvec_q8_multi (q/k/v, gate/up of a verify batch). */
+M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
+                                          hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Dequantization, row gather, vocab selection

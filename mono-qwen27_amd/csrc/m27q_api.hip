@@ -145,6 +145,37 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, swiglu, cfg, p, stream));
 }
 
+// Small-M products on int8 MFMA for TILED weights (m27q_mma.hip).
+m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
+                              const float *const *res, hipStream_t stream) {
+    for (int i = 0; i < n; ++i) {
+        const m27q_status st = check_weight(&ws[i], true);
+        if (st != M27Q_OK) return st;
+        if (!Ys[i]) return M27Q_ERR_NULL;
+        if (ws[i].ggml_type != ws[0].ggml_type) return M27Q_ERR_TYPE;
+        if (ws[i].layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
+        if (ws[i].row_blocks != ws[0].row_blocks) return M27Q_ERR_SHAPE;
+    }
+    if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    MatmulMultiParams p{};
+    p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
+    p.K = k_of(&ws[0]);
+    p.M = M;
+    if (matmul_mfma_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    const ActView a = act_view(xq, M, p.K);
+    p.xq = a.q;
+    p.xd = a.d;
+    p.xs = a.s;
+    p.nmat = n;
+    for (int i = 0; i < n; ++i) {
+        p.W[i] = (const uint8_t *)ws[i].ptr;
+        p.Y[i] = Ys[i];
+        p.res[i] = res[i];
+        p.rc[i] = (int)ws[i].row_count;
+    }
+    return hip_status(launch_matmul_mfma(ws[0].ggml_type, p, stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -264,7 +295,24 @@ M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq,
     p.xs = a.s;
     p.Y = Y;
     p.res = residual;
+    if (M == 1) return m27q_matvec_q8(w, xq, Y, residual, nullptr, stream);
+    if (w->layout == M27Q_LAYOUT_TILED) {
+        float *Ys[1] = {Y};
+        const float *rs[1] = {residual};
+        return matmul_multi_impl(1, w, M, xq, Ys, rs, stream);
+    }
     return hip_status(launch_matmul_q8(w->ggml_type, (int)w->layout, p, stream));
+}
+
+M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
+                                          hipStream_t stream) {
+    if (!ws || !Ys || !xq) return M27Q_ERR_NULL;
+    if (n < 1 || n > kMaxMulti || M < 1 || M > kMaxM) return M27Q_ERR_SHAPE;
+    for (int i = 0; i < n; ++i)
+        if (ws[i].layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
+    if (M == 1) return m27q_matvec_q8_multi(n, ws, xq, Ys, stream);
+    const float *rs[kMaxMulti] = {nullptr, nullptr, nullptr, nullptr};
+    return matmul_multi_impl(n, ws, M, xq, Ys, rs, stream);
 }
 
 static m27q_status gather_impl(const m27q_weight *w, const int32_t *ids, int row0, int n, float *out,

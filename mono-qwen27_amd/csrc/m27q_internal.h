@@ -73,6 +73,25 @@ struct MatmulParams {
     float *Y;
     const float *res;
 };
+
+// Small-M products over up to kMaxMulti weights that share the activation (same
+// type, layout and K), in one launch.
+struct MatmulMultiParams {
+    const uint8_t *W[kMaxMulti];
+    float *Y[kMaxMulti];
+    const float *res[kMaxMulti];
+    int rc[kMaxMulti];
+    int wg_start[kMaxMulti + 1];
+    int nmat;
+    int upr, K, M;
+    const int8_t *xq;
+    const float *xd;
+    const uint32_t *xs;
+};
 hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s);
+// int8-MFMA small-M products (m27q_mma.hip): TILED weights, any M (16 tokens
+// per launch).
+size_t matmul_mfma_lds_bytes(uint32_t type, int upr);
+hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
 
 }  // namespace m27q

@@ -1,0 +1,429 @@
+// m27q_mma.hip -- small-M products Y[M][N] = X[M][K] W[N][K]^T on int8 MFMA.
+//
+// For 2 <= M the per-lane dot4 path costs M times the M = 1 work and turns
+// compute-bound at once; here every 32-weight group of 16 weight rows and up
+// to 16 activation rows (tokens) is one v_mfma_i32_16x16x32_i8, which gives
+// the exact integer group sums for all token x row pairs.  The scales are
+// applied in fp32 afterwards: per group j, row r, token t
+//   Q4_K: d_r sc_rj dx_tj S_trj - dmin_r m_rj dx_tj sum(codes_tj)
+//   Q6_K: d_r dx_tj (sc_r,2j (S0 - 32 lo16_tj) + sc_r,2j+1 (S1 - 32 hi16_tj)),
+//         one MFMA per 16-value sub-block (the other half of the operand zero)
+//   Q8_0: d_r dx_tj S_trj
+// which are the per-group terms of the M = 1 products.
+//
+// Lane roles (v_mfma_i32_16x16x32_i8, layout checked on the device):
+//   A (activations): lane l holds token l % 16, K positions 8 q .. 8 q + 7 of
+//                    the group, q = l / 16;
+//   B (weights):     lane l holds row l % 16 of a 16-row tile, same positions;
+//   C:               lane l holds tokens 4 q .. 4 q + 3 of row l % 16.
+// Weights are read straight from the TILED layout (a 16-row tile is two 8-row
+// tiles), the token codes from the quantized activation buffer (L1/L2 hits:
+// every wave at the same K reads the same bytes), the activation scales from
+// LDS, staged transposed ([group][16 tokens]) so a lane reads its 4 tokens at
+// once.  K is split over the KS waves of a workgroup (as in the M = 1 GEMV);
+// each wave covers RT 16-row tiles, and the KS partials are reduced in LDS in a
+// fixed order.  Tokens beyond 16 are handled by further launches.
+//
+// No reference counterpart: the reference runs prefill and decode one token at
+// a time (src/mono27b_chat.cpp:399-403).
+#include <type_traits>
+
+#include "m27q_internal.h"
+#include "m27q_device.h"
+
+namespace m27q {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kMmaTok = 16;  // tokens per MFMA (padded with zeros)
+
+__device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+__device__ __forceinline__ v4i mfma32(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Activation scales of the lane's 4 tokens for one group, read from the
+// transposed LDS copy right where they are used.
+struct TokScales {
+    float4 d;
+    uint4 s;  // packed 16-value code sums
+};
+
+struct ScaleLds {
+    const float *dT;     // [groups][16 tokens]
+    const uint32_t *sT;  // [groups][16 tokens]
+    __device__ TokScales get(int g, int q) const {
+        return {*(const float4 *)(dT + g * 16 + 4 * q), *(const uint4 *)(sT + g * 16 + 4 * q)};
+    }
+};
+
+__device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
+__device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
+__device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+__device__ __forceinline__ uint32_t u4(const uint4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// ------------------------------------------------------------------ Q4_K --
+struct MmaQ4K {
+    static constexpr int kGroups = 8;  // 32-weight groups per unit
+    static constexpr int kUnitBytes = kQ4KUnit;
+    // second scale word: dx * (sum of the 32 codes), the min term's factor
+    __device__ static uint32_t stage_aux(float d, uint32_t s) { return __float_as_uint(d * (float)(s_lo(s) + s_hi(s))); }
+    struct Frag {
+        uint2 qs[4];  // bytes 32 g + 8 q .. +8 of the row's quants, g = 0..3
+        uint4 h;      // d | dmin, scales[12]
+    };
+    // unit: start of the 8-row TILED unit holding row i
+    __device__ static Frag load(const uint8_t *unit, int i, int q) {
+        Frag f;
+        const uint8_t *qs = unit + 128 + 128 * i + 8 * q;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) f.qs[g] = *(const uint2 *)(qs + 32 * g);
+        f.h = *(const uint4 *)(unit + 16 * i);
+        return f;
+    }
+    __device__ static long operand(const Frag &f, int j) {
+        const uint2 w = f.qs[j >> 1];
+        const int sh = 4 * (j & 1);
+        return as_long((w.x >> sh) & 0x0f0f0f0fu, (w.y >> sh) & 0x0f0f0f0fu);
+    }
+    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
+                                      float (&acc)[4]) {
+        // get_scale_min_k4 (exec:690-693) for all 8 pairs at once, one byte each
+        const uint32_t sc03 = f.h.y & 0x3f3f3f3fu, m03 = f.h.z & 0x3f3f3f3fu;
+        const uint32_t sc47 = (f.h.w & 0x0f0f0f0fu) | ((f.h.y >> 2) & 0x30303030u);
+        const uint32_t m47 = ((f.h.w >> 4) & 0x0f0f0f0fu) | ((f.h.z >> 2) & 0x30303030u);
+        const float d = f16_bits_to_f32(f.h.x), dmin = f16_bits_to_f32(f.h.x >> 16);
+        // Software pipeline: the MFMA of group j + 1 is issued before the scale
+        // arithmetic of group j; the scheduling barrier keeps every group's
+        // values local (hoisting all eight groups would need ~200 VGPRs).
+        v4i c = mfma32(a[0], operand(f, 0), v4i{0, 0, 0, 0});
+#pragma unroll
+        for (int j = 0; j < kGroups; ++j) {
+            v4i cn = c;
+            if (j + 1 < kGroups) cn = mfma32(a[j + 1], operand(f, j + 1), v4i{0, 0, 0, 0});
+            const uint32_t scw = j < 4 ? sc03 : sc47, mw = j < 4 ? m03 : m47;
+            const float ws = d * (float)((scw >> (8 * (j & 3))) & 0xffu);
+            const float wm = dmin * (float)((mw >> (8 * (j & 3))) & 0xffu);
+            const TokScales ts = sl.get(g0 + j, q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dx = f4(ts.d, e);
+                acc[e] = fmaf(ws, dx * (float)c[e], acc[e]);
+                acc[e] = fmaf(-wm, __uint_as_float(u4(ts.s, e)), acc[e]);
+            }
+            c = cn;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q6_K --
+struct MmaQ6K {
+    static constexpr int kGroups = 8;
+    static constexpr int kUnitBytes = kQ6KUnit;
+    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }  // the packed 16-value sums
+    struct Frag {
+        uint2 ql[2][2];  // [half h][r & 1]: ql bytes 64 h + 32 (r & 1) + 8 q .. +8
+        uint2 qh[2];     // [half h]: qh bytes 32 h + 8 q .. +8
+        uint4 sc;        // 16 int8 scales
+        uint32_t d;      // f16 bits
+    };
+    __device__ static Frag load(const uint8_t *unit, int i, int q) {
+        Frag f;
+        const uint8_t *ql = unit + kQ6KTQl + 128 * i + 8 * q;
+        const uint8_t *qh = unit + kQ6KTQh + 64 * i + 8 * q;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f.ql[h][0] = *(const uint2 *)(ql + 64 * h);
+            f.ql[h][1] = *(const uint2 *)(ql + 64 * h + 32);
+            f.qh[h] = *(const uint2 *)(qh + 32 * h);
+        }
+        f.sc = *(const uint4 *)(unit + kQ6KTSc + 16 * i);
+        f.d = *(const uint16_t *)(unit + kQ6KTD + 2 * i);
+        return f;
+    }
+    __device__ static int sc_byte(const uint4 &sc, int k) {
+        return (int)(int8_t)(u4(sc, k >> 2) >> (8 * (k & 3)));
+    }
+    // Group j = 4 h + r covers K 32 j .. 32 j + 31 of the block (half h, quarter r
+    // of the q6k_val index map, exec:1026-1048); sub-block 2 j (scale 8 h + 2 r)
+    // is held by lane quarters 0, 1 and sub-block 2 j + 1 by quarters 2, 3.
+    __device__ static long operand(const Frag &f, int j) {
+        const int h = j >> 2, r = j & 3;
+        const uint2 l = f.ql[h][r & 1], hb = f.qh[h];
+        const int nsh = 4 * (r >> 1), hsh = 2 * r;
+        const uint32_t b0 = ((l.x >> nsh) & 0x0f0f0f0fu) | (((hb.x >> hsh) & 0x03030303u) << 4);
+        const uint32_t b1 = ((l.y >> nsh) & 0x0f0f0f0fu) | (((hb.y >> hsh) & 0x03030303u) << 4);
+        return as_long(b0, b1);
+    }
+    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
+                                      float (&acc)[4]) {
+        const bool lo_quarter = q < 2;
+        const float d = f16_bits_to_f32(f.d);
+        // Two MFMAs per group, one per 16-value sub-block (the lane quarters
+        // holding the other sub-block pass zeros); pipelined as for Q4_K.
+        auto mm = [&](int j, v4i &c0, v4i &c1) {
+            const long b = operand(f, j);
+            c0 = mfma32(a[j], lo_quarter ? b : 0l, v4i{0, 0, 0, 0});
+            c1 = mfma32(a[j], lo_quarter ? 0l : b, v4i{0, 0, 0, 0});
+        };
+        v4i c0, c1;
+        mm(0, c0, c1);
+#pragma unroll
+        for (int j = 0; j < kGroups; ++j) {
+            v4i n0 = c0, n1 = c1;
+            if (j + 1 < kGroups) mm(j + 1, n0, n1);
+            const int h = j >> 2, r = j & 3;
+            const int s0 = sc_byte(f.sc, 8 * h + 2 * r), s1 = sc_byte(f.sc, 8 * h + 2 * r + 1);
+            const TokScales ts = sl.get(g0 + j, q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t s = u4(ts.s, e);
+                // the codes are q + 32: remove the offset with the exact code sums
+                const int v = __mul24(s0, c0[e] - 32 * s_lo(s)) + __mul24(s1, c1[e] - 32 * s_hi(s));
+                acc[e] = fmaf(d * f4(ts.d, e), (float)v, acc[e]);
+            }
+            c0 = n0;
+            c1 = n1;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q8_0 --
+struct MmaQ80 {
+    static constexpr int kGroups = 4;  // blocks of 32 per TILED unit
+    static constexpr int kUnitBytes = kQ80Unit;
+    __device__ static uint32_t stage_aux(float, uint32_t) { return 0u; }
+    struct Frag {
+        uint2 qs[4];
+        uint2 d;  // 4 f16 scales
+    };
+    __device__ static Frag load(const uint8_t *unit, int i, int q) {
+        Frag f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f.qs[k] = *(const uint2 *)(unit + 128 * i + 32 * k + 8 * q);
+        f.d = *(const uint2 *)(unit + kQ80TD + 8 * i);
+        return f;
+    }
+    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
+                                      float (&acc)[4]) {
+#pragma unroll
+        for (int j = 0; j < kGroups; ++j) {
+            const v4i c = mfma32(a[j], as_long(f.qs[j].x, f.qs[j].y), v4i{0, 0, 0, 0});
+            const float dw = f16_bits_to_f32(j < 2 ? (f.d.x >> (16 * j)) : (f.d.y >> (16 * (j - 2))));
+            const float4 dx = sl.get(g0 + j, q).d;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dw * f4(dx, e), (float)c[e], acc[e]);
+        }
+    }
+};
+
+// One unit (a K range of kGroups x 32) of activation operands.
+template <class T>
+struct ActUnit {
+    long a[T::kGroups];
+};
+
+// KS waves split K; each wave covers RT 16-row tiles.  Up to kMaxMulti weights
+// of one K share the launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
+template <class T, int KS, int RT>
+__global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, int m0) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int G = T::kGroups;
+    constexpr int TR = 16 * RT;  // weight rows per workgroup
+    const int lane = (int)(threadIdx.x & 63), q = lane >> 4, r16 = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    int mi = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMulti; ++k)
+        if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) mi = k;
+    const uint8_t *Wm = p.W[mi];
+    const int rc = p.rc[mi];
+    const int M = min(p.M - m0, kMmaTok);
+    const int ngroups = p.K / 32;
+    const int gpad = p.upr * G;  // groups of whole units (Q8_0 units can pass K)
+    const int ntiles8 = (rc + kTileRows - 1) / kTileRows;
+    const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * TR;
+
+    // Activation scales, transposed to [group][16 tokens] (zeros past M and K).
+    float *dT = (float *)smem;
+    uint32_t *sT = (uint32_t *)(smem + (size_t)gpad * kMmaTok * 4);
+    // Loads issued kBatch at a time before any is used: a few L2 round trips
+    // instead of one per entry.
+    constexpr int kBatch = 8;
+    for (int i0 = (int)threadIdx.x; i0 < gpad * kMmaTok; i0 += kBatch * KS * kWave) {
+        float d[kBatch];
+        uint32_t sw[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int idx = i0 + b * KS * kWave;
+            const int g = idx / kMmaTok, t = idx % kMmaTok;
+            const bool in = idx < gpad * kMmaTok && t < M && g < ngroups;
+            const size_t src = in ? (size_t)(m0 + t) * ngroups + g : 0;
+            d[b] = p.xd[src];
+            sw[b] = p.xs[src];
+            if (!in) {
+                d[b] = 0.f;
+                sw[b] = 0u;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int idx = i0 + b * KS * kWave;
+            if (idx < gpad * kMmaTok) {
+                dT[idx] = d[b];
+                sT[idx] = T::stage_aux(d[b], sw[b]);
+            }
+        }
+    }
+    const ScaleLds sl{dT, sT};
+    float *red = (float *)(smem + (size_t)gpad * kMmaTok * 8);  // [KS][16 tokens][TR]
+    __syncthreads();
+
+    // This wave's K slice (units) and the lane's rows.
+    const int U = p.upr / KS, rem = p.upr % KS;
+    const int ub = wave * U + min(wave, rem);
+    const int nu = U + (wave < rem ? 1 : 0);
+    const uint8_t *unit0[RT];
+    int irow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int row = row0 + 16 * t + r16;
+        const int tt = min(row / kTileRows, ntiles8 - 1);  // rows past the end: reread the last tile
+        unit0[t] = Wm + (size_t)tt * p.upr * T::kUnitBytes;
+        irow[t] = row % kTileRows;
+    }
+    const bool tok_in = r16 < M;
+    const int8_t *xrow = p.xq + (size_t)(m0 + (tok_in ? r16 : 0)) * p.K + 8 * q;
+
+    // Unconditional loads and a bit mask (a select on the loaded value would be
+    // turned into a branch around each load, with a wait inside it).
+    const uint32_t tmask = tok_in ? 0xffffffffu : 0u;
+    auto load_act = [&](ActUnit<T> &au, int u) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int g = u * G + j;
+            const uint2 v = *(const uint2 *)(xrow + (size_t)min(g, ngroups - 1) * 32);
+            const uint32_t msk = g < ngroups ? tmask : 0u;
+            au.a[j] = as_long(v.x & msk, v.y & msk);
+        }
+    };
+    auto load_w = [&](typename T::Frag (&f)[RT], int u) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) f[t] = T::load(unit0[t] + (size_t)u * T::kUnitBytes, irow[t], q);
+    };
+
+    float acc[RT][4];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
+
+    typename T::Frag fa[RT], fb[RT];
+    ActUnit<T> xa, xb;
+    const int u_first = min(ub, p.upr - 1);
+    load_w(fa, u_first);
+    load_act(xa, u_first);
+    int k = 0;
+    for (; k + 2 < nu; k += 2) {
+        load_w(fb, ub + k + 1);
+        load_act(xb, ub + k + 1);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
+        load_w(fa, ub + k + 2);
+        load_act(xa, ub + k + 2);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) T::accumulate(fb[t], xb.a, sl, (ub + k + 1) * G, q, acc[t]);
+    }
+    if (k + 1 < nu) {
+        load_w(fb, ub + k + 1);
+        load_act(xb, ub + k + 1);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) T::accumulate(fb[t], xb.a, sl, (ub + k + 1) * G, q, acc[t]);
+    } else if (k < nu) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
+    }
+
+    // Partials of this wave's K slice -> LDS, then one thread per (token, row).
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[((size_t)wave * kMmaTok + 4 * q + e) * TR + 16 * t + r16] = acc[t][e];
+    __syncthreads();
+    for (int idx = (int)threadIdx.x; idx < M * TR; idx += KS * kWave) {
+        const int tok = idx / TR, rr = idx % TR, row = row0 + rr;
+        float v = red[(size_t)tok * TR + rr];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) v += red[((size_t)w * kMmaTok + tok) * TR + rr];
+        if (row < rc) {
+            const size_t o = (size_t)(m0 + tok) * rc + row;
+            p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
+        }
+    }
+}
+
+template <class T, int KS, int RT>
+static size_t mfma_lds(int upr) {
+    return (size_t)upr * T::kGroups * kMmaTok * 8 + (size_t)KS * kMmaTok * 16 * RT * 4;
+}
+
+template <class T, int KS>
+static hipError_t launch_mfma_t(MatmulMultiParams p, hipStream_t s) {
+    constexpr int RT = 1;
+    const size_t lds = mfma_lds<T, KS, RT>(p.upr);
+    int total = 0;
+    for (int i = 0; i < p.nmat; ++i) {
+        p.wg_start[i] = total;
+        total += (p.rc[i] + 16 * RT - 1) / (16 * RT);
+    }
+    p.wg_start[p.nmat] = total;
+    for (int m0 = 0; m0 < p.M; m0 += kMmaTok) {
+        hipLaunchKernelGGL((k_matmul_mfma<T, KS, RT>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Waves per workgroup (K slices) so that a launch has a few thousand waves:
+// one wave streams one 16-row tile of its K slice.
+static int mfma_ks(const MatmulMultiParams &p) {
+    long long tiles = 0;
+    for (int i = 0; i < p.nmat; ++i) tiles += (p.rc[i] + 15) / 16;
+    if (tiles >= 1024) return 4;
+    if (tiles >= 256) return 8;
+    return 16;
+}
+
+template <class T>
+static hipError_t launch_mfma_ks(const MatmulMultiParams &p, hipStream_t s) {
+    switch (mfma_ks(p)) {
+        case 4: return launch_mfma_t<T, 4>(p, s);
+        case 8: return launch_mfma_t<T, 8>(p, s);
+        default: return launch_mfma_t<T, 16>(p, s);
+    }
+}
+
+size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
+    switch (type) {
+        case kQ4_K: return mfma_lds<MmaQ4K, 16, 1>(upr);
+        case kQ6_K: return mfma_lds<MmaQ6K, 16, 1>(upr);
+        case kQ8_0: return mfma_lds<MmaQ80, 16, 1>(upr);
+        default: return 0;
+    }
+}
+
+hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_mfma_ks<MmaQ4K>(p, s);
+        case kQ6_K: return launch_mfma_ks<MmaQ6K>(p, s);
+        case kQ8_0: return launch_mfma_ks<MmaQ80>(p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace m27q

@@ -57,6 +57,7 @@ _SIGS = {
     "m27q_matvec_f32": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P]),
     "m27q_matvec": (_I, [C.POINTER(WeightDesc), _P, _P, _P, _P, _P]),
     "m27q_matmul_q8": (_I, [C.POINTER(WeightDesc), _I, _P, _P, _P, _P]),
+    "m27q_matmul_q8_multi": (_I, [_I, C.POINTER(WeightDesc), _I, _P, C.POINTER(_P), _P]),
     "m27q_dequant_rows": (_I, [C.POINTER(WeightDesc), _I, _I, _P, _P]),
     "m27q_embed_rows": (_I, [C.POINTER(WeightDesc), _P, _I, _P, _P, _P]),
     "m27q_embed_token": (_I, [C.POINTER(WeightDesc), C.c_int32, _P, _P]),
@@ -246,6 +247,13 @@ def matmul_q8(w: Weight, act: Act, Y, residual=None, stream=None) -> None:
     d = w.desc()
     check(lib().m27q_matmul_q8(C.byref(d), act.M, _ptr(act.buf), _ptr(Y), _ptr(residual), _stream(stream)),
           "m27q_matmul_q8")
+
+
+def matmul_q8_multi(ws: list[Weight], act: Act, Ys: list, stream=None) -> None:
+    n = len(ws)
+    descs = (WeightDesc * n)(*[w.desc() for w in ws])
+    yp = (C.c_void_p * n)(*[_ptr(y) for y in Ys])
+    check(lib().m27q_matmul_q8_multi(n, descs, act.M, _ptr(act.buf), yp, _stream(stream)), "m27q_matmul_q8_multi")
 
 
 def dequant_rows(w: Weight, row0: int, nrows: int, out, stream=None) -> None:

@@ -40,3 +40,25 @@ def test_matmul_vs_oracle(m27q, ora, dev, type_name, rc, k, M, layout):
     for m in rows:
         want, nrm = ora.gemv_act(t, wb, rb, rc, q[m], d[m], s[m])
         assert (np.abs(got[m] - want) <= int_dot_tol(nrm) + 1e-6 * np.abs(res[m])).all(), m
+
+
+@pytest.mark.parametrize("M", [2, 16, 19])
+def test_matmul_multi_vs_oracle(m27q, ora, dev, M):
+    """q/k/v-shaped weights on one activation in one launch, each against the
+    integer-dot oracle (row subsets), across the 16-token launch boundary."""
+    import torch
+    k, shapes = 5120, [6144, 1024, 1024]
+    wbs = [ora.synth_weights(m27q.Q4_K, rc, k, seed=60 + i) for i, rc in enumerate(shapes)]
+    ws = [m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 20, rc, m27q.TILED, dev) for wb, rc in zip(wbs, shapes)]
+    X = np.random.default_rng(M + 7).standard_normal((M, k)).astype(np.float32)
+    act = m27q.Act(M, k, dev)
+    m27q.quant_act(to_dev(X, dev), act)
+    Ys = [torch.empty((M, rc), dtype=torch.float32, device=dev) for rc in shapes]
+    say("matmul multi", M)
+    m27q.matmul_q8_multi(ws, act, Ys)
+    q, d, s = act_host(m27q, act)
+    for wb, rc, Y in zip(wbs, shapes, Ys):
+        got = to_host(Y).astype(np.float64)
+        for m in sorted({0, M // 2, M - 1}):
+            want, nrm = ora.gemv_act(m27q.Q4_K, wb, 20, rc, q[m], d[m], s[m])
+            assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)
