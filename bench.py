@@ -191,11 +191,12 @@ def suite(m27q, torch, dev, layers, reps):
     scratch = torch.empty(m27q.topk_scratch_bytes(248320, k), dtype=torch.uint8, device=dev)
     idx = torch.empty(k, dtype=torch.int32, device=dev)
     val = torch.empty(k, dtype=torch.float32, device=dev)
-    us = timed(torch, lambda c, st: m27q.topk(logits, k, idx, val, scratch, stream=st), 1, reps)
+    # 16 calls per graph replay, so the host's replay cost stays hidden behind the GPU
+    us = timed(torch, lambda c, st: m27q.topk(logits, k, idx, val, scratch, stream=st), 16, reps)
     out["cfg5_topk64_of_248320"] = {"us": round(us, 3), "GBps": round(248320 * 4 / us / 1e3, 1)}
-    ids = torch.from_numpy(rng.integers(0, 248320, 512).astype(np.int32)).to(dev)
+    ids = [torch.from_numpy(rng.integers(0, 248320, 512).astype(np.int32)).to(dev) for _ in range(16)]
     rows = torch.empty((512, 5120), dtype=torch.float32, device=dev)
-    us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids, rows, stream=st), 1, reps)
+    us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids[c], rows, stream=st), 16, reps)
     out["cfg5_gather_512_q6k_rows"] = {"us": round(us, 3), "GBps": round((512 * 4200 + 512 * 5120 * 4) / us / 1e3, 1)}
     log("config 5 done")
     return out

@@ -34,6 +34,7 @@
 namespace m27q {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kMmaTok = 16;  // tokens per MFMA (padded with zeros)
 
 __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
@@ -41,20 +42,17 @@ __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long
 __device__ __forceinline__ v4i mfma32(long a, long b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
-// Activation scales of the lane's 4 tokens for one group, read from the
-// transposed LDS copy right where they are used.
-struct TokScales {
-    float4 d;
-    uint4 s;  // packed 16-value code sums
-};
-
+// Activation scales in LDS, transposed to [group][16 tokens]: a lane reads the
+// dx of its 4 tokens (4 q .. 4 q + 3) with one 16-byte read.
 struct ScaleLds {
     const float *dT;     // [groups][16 tokens]
-    const uint32_t *sT;  // [groups][16 tokens]
-    __device__ TokScales get(int g, int q) const {
-        return {*(const float4 *)(dT + g * 16 + 4 * q), *(const uint4 *)(sT + g * 16 + 4 * q)};
-    }
+    const float *aT;     // [groups][16 tokens], the type's per-group token term (Q4_K only)
+    __device__ float4 dx(int g, int q) const { return *(const float4 *)(dT + g * 16 + 4 * q); }
+    __device__ float aux(int g, int tok) const { return aT[g * 16 + tok]; }
 };
 
 __device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
@@ -66,8 +64,9 @@ __device__ __forceinline__ uint32_t u4(const uint4 &v, int e) { return e == 0 ? 
 struct MmaQ4K {
     static constexpr int kGroups = 8;  // 32-weight groups per unit
     static constexpr int kUnitBytes = kQ4KUnit;
-    // second scale word: dx * (sum of the 32 codes), the min term's factor
-    __device__ static uint32_t stage_aux(float d, uint32_t s) { return __float_as_uint(d * (float)(s_lo(s) + s_hi(s))); }
+    static constexpr bool kAux = true;
+    // The min term's token factor: dx * (sum of the 32 codes).
+    __device__ static float stage_aux(float d, uint32_t s) { return d * (float)(s_lo(s) + s_hi(s)); }
     struct Frag {
         uint2 qs[4];  // bytes 32 g + 8 q .. +8 of the row's quants, g = 0..3
         uint4 h;      // d | dmin, scales[12]
@@ -86,32 +85,49 @@ struct MmaQ4K {
         const int sh = 4 * (j & 1);
         return as_long((w.x >> sh) & 0x0f0f0f0fu, (w.y >> sh) & 0x0f0f0f0fu);
     }
-    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
-                                      float (&acc)[4]) {
-        // get_scale_min_k4 (exec:690-693) for all 8 pairs at once, one byte each
-        const uint32_t sc03 = f.h.y & 0x3f3f3f3fu, m03 = f.h.z & 0x3f3f3f3fu;
-        const uint32_t sc47 = (f.h.w & 0x0f0f0f0fu) | ((f.h.y >> 2) & 0x30303030u);
-        const uint32_t m47 = ((f.h.w >> 4) & 0x0f0f0f0fu) | ((f.h.z >> 2) & 0x30303030u);
-        const float d = f16_bits_to_f32(f.h.x), dmin = f16_bits_to_f32(f.h.x >> 16);
-        // Software pipeline: the MFMA of group j + 1 is issued before the scale
-        // arithmetic of group j; the scheduling barrier keeps every group's
-        // values local (hoisting all eight groups would need ~200 VGPRs).
-        v4i c = mfma32(a[0], operand(f, 0), v4i{0, 0, 0, 0});
+    // Main term: acc[t][e] += d sc_j * dx_j,e * S_j,e per group (VALU, the
+    // group's integer sums from the MFMA).  Min term: cm[t] += sum_j aux_j,tok *
+    // (dmin m_j,row), an fp32 MFMA over the unit's 8 groups (2 x K = 4).
+    template <int RT>
+    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
+                                      int q, int r16, float (&acc)[RT][4], v4f (&cm)[RT]) {
+        uint32_t scA[RT], scB[RT];
+        float d[RT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            // get_scale_min_k4 (exec:690-693) for all 8 pairs at once, one byte each
+            const uint4 h = f[t].h;
+            scA[t] = h.y & 0x3f3f3f3fu;
+            scB[t] = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+            const uint32_t m03 = h.z & 0x3f3f3f3fu;
+            const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+            d[t] = f16_bits_to_f32(h.x);
+            const float dmin = f16_bits_to_f32(h.x >> 16);
+            const float b0 = dmin * (float)((m03 >> (8 * q)) & 0xffu);
+            const float b1 = dmin * (float)((m47 >> (8 * q)) & 0xffu);
+            cm[t] = mfma_f32(sl.aux(g0 + q, r16), b0, cm[t]);
+            cm[t] = mfma_f32(sl.aux(g0 + 4 + q, r16), b1, cm[t]);
+        }
+        // Software pipeline: the MFMAs of group j + 1 are issued before the
+        // scale arithmetic of group j; the scheduling barrier keeps each group's
+        // values local.
+        v4i c[RT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) c[t] = mfma32(a[0], operand(f[t], 0), v4i{0, 0, 0, 0});
 #pragma unroll
         for (int j = 0; j < kGroups; ++j) {
-            v4i cn = c;
-            if (j + 1 < kGroups) cn = mfma32(a[j + 1], operand(f, j + 1), v4i{0, 0, 0, 0});
-            const uint32_t scw = j < 4 ? sc03 : sc47, mw = j < 4 ? m03 : m47;
-            const float ws = d * (float)((scw >> (8 * (j & 3))) & 0xffu);
-            const float wm = dmin * (float)((mw >> (8 * (j & 3))) & 0xffu);
-            const TokScales ts = sl.get(g0 + j, q);
+            v4i cn[RT];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float dx = f4(ts.d, e);
-                acc[e] = fmaf(ws, dx * (float)c[e], acc[e]);
-                acc[e] = fmaf(-wm, __uint_as_float(u4(ts.s, e)), acc[e]);
+            for (int t = 0; t < RT; ++t) cn[t] = j + 1 < kGroups ? mfma32(a[j + 1], operand(f[t], j + 1), v4i{0, 0, 0, 0}) : c[t];
+            const float4 dx = sl.dx(g0 + j, q);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const uint32_t scw = j < 4 ? scA[t] : scB[t];
+                const float ws = d[t] * (float)((scw >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(ws, f4(dx, e) * (float)c[t][e], acc[t][e]);
+                c[t] = cn[t];
             }
-            c = cn;
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -121,7 +137,8 @@ struct MmaQ4K {
 struct MmaQ6K {
     static constexpr int kGroups = 8;
     static constexpr int kUnitBytes = kQ6KUnit;
-    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }  // the packed 16-value sums
+    static constexpr bool kAux = false;
+    __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     struct Frag {
         uint2 ql[2][2];  // [half h][r & 1]: ql bytes 64 h + 32 (r & 1) + 8 q .. +8
         uint2 qh[2];     // [half h]: qh bytes 32 h + 8 q .. +8
@@ -148,44 +165,66 @@ struct MmaQ6K {
     // Group j = 4 h + r covers K 32 j .. 32 j + 31 of the block (half h, quarter r
     // of the q6k_val index map, exec:1026-1048); sub-block 2 j (scale 8 h + 2 r)
     // is held by lane quarters 0, 1 and sub-block 2 j + 1 by quarters 2, 3.
+    // The 6-bit codes b become the signed q = b - 32 per byte:
+    // (b + 0x60) ^ 0x80 = b - 32 (mod 256) for 0 <= b <= 63, with no carry
+    // between bytes.
     __device__ static long operand(const Frag &f, int j) {
         const int h = j >> 2, r = j & 3;
         const uint2 l = f.ql[h][r & 1], hb = f.qh[h];
         const int nsh = 4 * (r >> 1), hsh = 2 * r;
-        const uint32_t b0 = ((l.x >> nsh) & 0x0f0f0f0fu) | (((hb.x >> hsh) & 0x03030303u) << 4);
-        const uint32_t b1 = ((l.y >> nsh) & 0x0f0f0f0fu) | (((hb.y >> hsh) & 0x03030303u) << 4);
-        return as_long(b0, b1);
+        const uint32_t b0 = ((l.x >> nsh) & 0x0f0f0f0fu) + (((hb.x >> hsh) & 0x03030303u) << 4) + 0x60606060u;
+        const uint32_t b1 = ((l.y >> nsh) & 0x0f0f0f0fu) + (((hb.y >> hsh) & 0x03030303u) << 4) + 0x60606060u;
+        return as_long(b0 ^ 0x80808080u, b1 ^ 0x80808080u);
     }
-    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
-                                      float (&acc)[4]) {
+    // acc[t][e] += d * sum_j dx_j,e (sc_2j S0_j,e + sc_2j+1 S1_j,e); the group
+    // sums are exact integers, d is applied once per unit.
+    template <int RT>
+    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
+                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
         const bool lo_quarter = q < 2;
-        const float d = f16_bits_to_f32(f.d);
+        float u[RT][4];
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[t][e] = 0.f;
         // Two MFMAs per group, one per 16-value sub-block (the lane quarters
         // holding the other sub-block pass zeros); pipelined as for Q4_K.
-        auto mm = [&](int j, v4i &c0, v4i &c1) {
-            const long b = operand(f, j);
-            c0 = mfma32(a[j], lo_quarter ? b : 0l, v4i{0, 0, 0, 0});
-            c1 = mfma32(a[j], lo_quarter ? 0l : b, v4i{0, 0, 0, 0});
+        v4i c0[RT], c1[RT];
+        auto mm = [&](int j, v4i (&x0)[RT], v4i (&x1)[RT]) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const long b = operand(f[t], j);
+                x0[t] = mfma32(a[j], lo_quarter ? b : 0l, v4i{0, 0, 0, 0});
+                x1[t] = mfma32(a[j], lo_quarter ? 0l : b, v4i{0, 0, 0, 0});
+            }
         };
-        v4i c0, c1;
         mm(0, c0, c1);
 #pragma unroll
         for (int j = 0; j < kGroups; ++j) {
-            v4i n0 = c0, n1 = c1;
+            v4i n0[RT], n1[RT];
             if (j + 1 < kGroups) mm(j + 1, n0, n1);
             const int h = j >> 2, r = j & 3;
-            const int s0 = sc_byte(f.sc, 8 * h + 2 * r), s1 = sc_byte(f.sc, 8 * h + 2 * r + 1);
-            const TokScales ts = sl.get(g0 + j, q);
+            const float4 dx = sl.dx(g0 + j, q);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t s = u4(ts.s, e);
-                // the codes are q + 32: remove the offset with the exact code sums
-                const int v = __mul24(s0, c0[e] - 32 * s_lo(s)) + __mul24(s1, c1[e] - 32 * s_hi(s));
-                acc[e] = fmaf(d * f4(ts.d, e), (float)v, acc[e]);
+            for (int t = 0; t < RT; ++t) {
+                const int s0 = sc_byte(f[t].sc, 8 * h + 2 * r), s1 = sc_byte(f[t].sc, 8 * h + 2 * r + 1);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = __mul24(s0, c0[t][e]) + __mul24(s1, c1[t][e]);
+                    u[t][e] = fmaf(f4(dx, e), (float)v, u[t][e]);
+                }
+                if (j + 1 < kGroups) {
+                    c0[t] = n0[t];
+                    c1[t] = n1[t];
+                }
             }
-            c0 = n0;
-            c1 = n1;
             __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const float d = f16_bits_to_f32(f[t].d);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(d, u[t][e], acc[t][e]);
         }
     }
 };
@@ -194,7 +233,8 @@ struct MmaQ6K {
 struct MmaQ80 {
     static constexpr int kGroups = 4;  // blocks of 32 per TILED unit
     static constexpr int kUnitBytes = kQ80Unit;
-    __device__ static uint32_t stage_aux(float, uint32_t) { return 0u; }
+    static constexpr bool kAux = false;
+    __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     struct Frag {
         uint2 qs[4];
         uint2 d;  // 4 f16 scales
@@ -206,15 +246,20 @@ struct MmaQ80 {
         f.d = *(const uint2 *)(unit + kQ80TD + 8 * i);
         return f;
     }
-    __device__ static void accumulate(const Frag &f, const long (&a)[kGroups], const ScaleLds &sl, int g0, int q,
-                                      float (&acc)[4]) {
+    template <int RT>
+    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
+                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
 #pragma unroll
         for (int j = 0; j < kGroups; ++j) {
-            const v4i c = mfma32(a[j], as_long(f.qs[j].x, f.qs[j].y), v4i{0, 0, 0, 0});
-            const float dw = f16_bits_to_f32(j < 2 ? (f.d.x >> (16 * j)) : (f.d.y >> (16 * (j - 2))));
-            const float4 dx = sl.get(g0 + j, q).d;
+            const float4 dx = sl.dx(g0 + j, q);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dw * f4(dx, e), (float)c[e], acc[e]);
+            for (int t = 0; t < RT; ++t) {
+                const v4i c = mfma32(a[j], as_long(f[t].qs[j].x, f[t].qs[j].y), v4i{0, 0, 0, 0});
+                const uint32_t dw2 = j < 2 ? f[t].d.x : f[t].d.y;
+                const float dw = f16_bits_to_f32(dw2 >> (16 * (j & 1)));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(dw * f4(dx, e), (float)c[e], acc[t][e]);
+            }
         }
     }
 };
@@ -246,9 +291,10 @@ __global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, 
     const int ntiles8 = (rc + kTileRows - 1) / kTileRows;
     const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * TR;
 
-    // Activation scales, transposed to [group][16 tokens] (zeros past M and K).
+    // Activation scales, transposed to [group][16 tokens] (zeros past M and K),
+    // and for Q4_K the min term's token factor in the same shape.
     float *dT = (float *)smem;
-    uint32_t *sT = (uint32_t *)(smem + (size_t)gpad * kMmaTok * 4);
+    float *aT = (float *)(smem + (size_t)gpad * kMmaTok * 4);
     // Loads issued kBatch at a time before any is used: a few L2 round trips
     // instead of one per entry.
     constexpr int kBatch = 8;
@@ -262,7 +308,7 @@ __global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, 
             const bool in = idx < gpad * kMmaTok && t < M && g < ngroups;
             const size_t src = in ? (size_t)(m0 + t) * ngroups + g : 0;
             d[b] = p.xd[src];
-            sw[b] = p.xs[src];
+            sw[b] = T::kAux ? p.xs[src] : 0u;
             if (!in) {
                 d[b] = 0.f;
                 sw[b] = 0u;
@@ -273,12 +319,12 @@ __global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, 
             const int idx = i0 + b * KS * kWave;
             if (idx < gpad * kMmaTok) {
                 dT[idx] = d[b];
-                sT[idx] = T::stage_aux(d[b], sw[b]);
+                if (T::kAux) aT[idx] = T::stage_aux(d[b], sw[b]);
             }
         }
     }
-    const ScaleLds sl{dT, sT};
-    float *red = (float *)(smem + (size_t)gpad * kMmaTok * 8);  // [KS][16 tokens][TR]
+    const ScaleLds sl{dT, aT};
+    float *red = (float *)(smem + (size_t)gpad * kMmaTok * (T::kAux ? 8 : 4));  // [KS][16 tokens][TR]
     __syncthreads();
 
     // This wave's K slice (units) and the lane's rows.
@@ -315,37 +361,53 @@ __global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, 
     };
 
     float acc[RT][4];
+    v4f cm[RT];  // Q4_K min term
 #pragma unroll
-    for (int t = 0; t < RT; ++t)
+    for (int t = 0; t < RT; ++t) {
+        cm[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
+    }
+    auto step = [&](const typename T::Frag (&f)[RT], const ActUnit<T> &x, int u) {
+        T::template accumulate<RT>(f, x.a, sl, u * G, q, r16, acc, cm);
+    };
 
     typename T::Frag fa[RT], fb[RT];
     ActUnit<T> xa, xb;
-    const int u_first = min(ub, p.upr - 1);
+#ifdef M27Q_MFMA_STAGGER
+    const int rot = nu > 0 ? (int)(blockIdx.x % (unsigned)nu) : 0;
+#else
+    const int rot = 0;
+#endif
+    auto uid = [&](int k) {
+        const int v = k + rot;
+        return ub + (v >= nu ? v - nu : v);
+    };
+    const int u_first = nu > 0 ? uid(0) : min(ub, p.upr - 1);
     load_w(fa, u_first);
     load_act(xa, u_first);
     int k = 0;
     for (; k + 2 < nu; k += 2) {
-        load_w(fb, ub + k + 1);
-        load_act(xb, ub + k + 1);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
-        load_w(fa, ub + k + 2);
-        load_act(xa, ub + k + 2);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) T::accumulate(fb[t], xb.a, sl, (ub + k + 1) * G, q, acc[t]);
+        load_w(fb, uid(k + 1));
+        load_act(xb, uid(k + 1));
+        step(fa, xa, uid(k));
+        load_w(fa, uid(k + 2));
+        load_act(xa, uid(k + 2));
+        step(fb, xb, uid(k + 1));
     }
     if (k + 1 < nu) {
-        load_w(fb, ub + k + 1);
-        load_act(xb, ub + k + 1);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) T::accumulate(fb[t], xb.a, sl, (ub + k + 1) * G, q, acc[t]);
+        load_w(fb, uid(k + 1));
+        load_act(xb, uid(k + 1));
+        step(fa, xa, uid(k));
+        step(fb, xb, uid(k + 1));
     } else if (k < nu) {
+        step(fa, xa, uid(k));
+    }
+    if (T::kAux) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t) T::accumulate(fa[t], xa.a, sl, (ub + k) * G, q, acc[t]);
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][e] -= cm[t][e];
     }
 
     // Partials of this wave's K slice -> LDS, then one thread per (token, row).
@@ -368,12 +430,11 @@ __global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, 
 
 template <class T, int KS, int RT>
 static size_t mfma_lds(int upr) {
-    return (size_t)upr * T::kGroups * kMmaTok * 8 + (size_t)KS * kMmaTok * 16 * RT * 4;
+    return (size_t)upr * T::kGroups * kMmaTok * (T::kAux ? 8 : 4) + (size_t)KS * kMmaTok * 16 * RT * 4;
 }
 
-template <class T, int KS>
+template <class T, int KS, int RT>
 static hipError_t launch_mfma_t(MatmulMultiParams p, hipStream_t s) {
-    constexpr int RT = 1;
     const size_t lds = mfma_lds<T, KS, RT>(p.upr);
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
@@ -389,23 +450,25 @@ static hipError_t launch_mfma_t(MatmulMultiParams p, hipStream_t s) {
     return hipSuccess;
 }
 
-// Waves per workgroup (K slices) so that a launch has a few thousand waves:
-// one wave streams one 16-row tile of its K slice.
-static int mfma_ks(const MatmulMultiParams &p) {
+// Launch shape: RT 16-row tiles per wave share each activation load and LDS
+// scale read; K is split over KS waves so that a launch still has a few
+// thousand waves.  KS * RT <= 16 keeps the LDS within the KS = 16, RT = 1 size
+// the caller checks.
+template <class T>
+static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
+#if defined(M27Q_MFMA_KS) && defined(M27Q_MFMA_RT)
+    static_assert(M27Q_MFMA_KS * M27Q_MFMA_RT <= 16, "LDS bound");
+    return launch_mfma_t<T, M27Q_MFMA_KS, M27Q_MFMA_RT>(p, s);
+#else
+    // Measured on the Qwen-27B layer (M = 2 .. 16): (4, 2) for gate/up
+    // (2176 tiles) and down (320 tiles, Q6_K), (8, 2) for q/k/v and o (512
+    // and 320 tiles, Q4_K); RT = 4 runs at one wave per SIMD.
     long long tiles = 0;
     for (int i = 0; i < p.nmat; ++i) tiles += (p.rc[i] + 15) / 16;
-    if (tiles >= 1024) return 4;
-    if (tiles >= 256) return 8;
-    return 16;
-}
-
-template <class T>
-static hipError_t launch_mfma_ks(const MatmulMultiParams &p, hipStream_t s) {
-    switch (mfma_ks(p)) {
-        case 4: return launch_mfma_t<T, 4>(p, s);
-        case 8: return launch_mfma_t<T, 8>(p, s);
-        default: return launch_mfma_t<T, 16>(p, s);
-    }
+    if (tiles >= 1024 || (std::is_same<T, MmaQ6K>::value && tiles >= 256)) return launch_mfma_t<T, 4, 2>(p, s);
+    if (tiles >= 256) return launch_mfma_t<T, 8, 2>(p, s);
+    return launch_mfma_t<T, 16, 1>(p, s);
+#endif
 }
 
 size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
@@ -419,9 +482,9 @@ size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
 
 hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_mfma_ks<MmaQ4K>(p, s);
-        case kQ6_K: return launch_mfma_ks<MmaQ6K>(p, s);
-        case kQ8_0: return launch_mfma_ks<MmaQ80>(p, s);
+        case kQ4_K: return launch_mfma_cfg<MmaQ4K>(p, s);
+        case kQ6_K: return launch_mfma_cfg<MmaQ6K>(p, s);
+        case kQ8_0: return launch_mfma_cfg<MmaQ80>(p, s);
         default: return hipErrorInvalidValue;
     }
 }
