@@ -6,12 +6,19 @@
 // keys is (value desc, index asc), all keys are distinct, and no key is 0
 // (0 marks an empty slot).
 //
-// Selection is a radix select on the keys, 8 bits per pass from the top, with
-// a 256-bin histogram in LDS: each pass narrows the prefix of the k-th largest
-// key until the keys sharing it are exactly the ones still needed; the k keys
-// at or above that prefix are then compacted.  Pass 1 (one workgroup per chunk
-// of the vector) writes each chunk's top k; pass 2 (one workgroup) selects the
-// top k of those and sorts them with a wavefront bitonic sort.
+// Three launches:
+//   1. chunk maxima: workgroup c writes the largest key of its chunk;
+//   2. filter: every workgroup takes T = the k-th largest chunk maximum (k
+//      chunks hold a key >= T, so the k-th largest key overall is >= T) and
+//      appends the keys >= T of its chunk to a candidate list, reserving its
+//      slots with one atomic on a counter;
+//      A chunk with more than k such keys first reduces them to its own top k
+//      (radix select within the workgroup), so the list never exceeds
+//      nchunks * k keys;
+//   3. select (one workgroup): with at most 1024 candidates (the usual case:
+//      about 75 for 248320 i.i.d. logits) each candidate's rank is counted
+//      directly and the first k are written in rank order; with more, a radix
+//      select runs over the candidates.
 // Replaces the CPU selection of sample() (src/mono27b_chat.cpp:211-227) and
 // k_argmax (exec:211-239).
 #include "m27q_internal.h"
@@ -19,10 +26,11 @@
 
 namespace m27q {
 
-constexpr int kTopkBlock1 = 256;   // threads of a pass-1 workgroup
-constexpr int kTopkBlock2 = 1024;  // threads of the pass-2 workgroup
+constexpr int kTopkBlock = 256;      // threads of a chunk workgroup
+constexpr int kTopkSelBlock = 1024;  // threads of the select workgroup
 constexpr int kTopkMaxK = 64;
-constexpr int kTopkMaxChunks = 256;  // pass-2 capacity: 256 x 64 keys = 16 per thread
+constexpr int kTopkMaxChunks = 256;
+constexpr int kTopkCap = kTopkMaxChunks * kTopkMaxK;  // candidate list capacity
 
 __device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
     uint32_t o = 0u;  // NaN
@@ -33,17 +41,62 @@ __device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
     return ((uint64_t)o << 32) | (uint64_t)(~idx);
 }
 
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, mask, kWave);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), mask, kWave);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Scratch layout: chunk maxima, the candidate counter, the candidates.
+struct TopkScratch {
+    uint64_t *maxkey;  // [kTopkMaxChunks]
+    uint32_t *count;   // one counter (8-byte slot)
+    uint64_t *cand;    // [kTopkCap]
+};
+__host__ __device__ inline TopkScratch topk_scratch(void *base) {
+    uint64_t *p = (uint64_t *)base;
+    return {p, (uint32_t *)(p + kTopkMaxChunks), p + kTopkMaxChunks + 1};
+}
+
+// 1. Largest key of each chunk; workgroup 0 also clears the counter (the
+// launches run in stream order, so the filter sees it cleared).
+__global__ __launch_bounds__(kTopkBlock) void k_topk_chunk_max(const float *__restrict__ v, int n, int chunk,
+                                                               TopkScratch sc) {
+    __shared__ uint64_t wmax[kTopkBlock / kWave];
+    const long long base = (long long)blockIdx.x * chunk;
+    const int end = (int)min((long long)n, base + chunk);
+    uint64_t m = 0;
+    for (int i = (int)base + (int)threadIdx.x; i < end; i += kTopkBlock) {
+        const uint64_t key = topk_key(v[i], (uint32_t)i);
+        m = key > m ? key : m;
+    }
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+        const uint64_t o = shfl_xor64(m, s);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t r = wmax[0];
+#pragma unroll
+        for (int w = 1; w < kTopkBlock / kWave; ++w) r = wmax[w] > r ? wmax[w] : r;
+        sc.maxkey[blockIdx.x] = r;
+        if (blockIdx.x == 0) *sc.count = 0u;
+    }
+}
+
 struct SelectShared {
     uint32_t hist[256];
     uint32_t above[256];
     int need, done, count;
-    uint64_t prefix, minkey;
+    uint64_t prefix;
     int shift;
 };
 
-// hist[bin] += 1 for every active lane.  Logits crowd into a few bins at the
-// top digits, where plain LDS atomics on one address serialize lane by lane:
-// the first lanes' bins are counted with one ballot each, the rest atomically.
+// hist[bin] += 1 for every active lane; the first lanes' bins are counted with
+// one ballot each (keys crowd into a few bins at the top digits), the rest with
+// LDS atomics.
 __device__ __forceinline__ void hist_add(uint32_t *hist, bool active, uint32_t bin) {
     const int lane = (int)(threadIdx.x & (kWave - 1));
 #pragma unroll
@@ -51,7 +104,7 @@ __device__ __forceinline__ void hist_add(uint32_t *hist, bool active, uint32_t b
         const uint64_t m = __ballot(active);
         if (m == 0) return;  // wave-uniform
         const int leader = __ffsll((long long)m) - 1;
-        const uint32_t lb = (uint32_t)__shfl((int)bin, leader, kWave);
+        const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
         const bool same = active && bin == lb;
         const uint64_t sm = __ballot(same);
         if (lane == leader) atomicAdd(&hist[lb], (uint32_t)__popcll(sm));
@@ -60,15 +113,13 @@ __device__ __forceinline__ void hist_add(uint32_t *hist, bool active, uint32_t b
     if (active) atomicAdd(&hist[bin], 1u);
 }
 
-// Select the k largest of the keys held by the block (KPT per thread, 0 =
-// empty) and write them, in no particular order, to out[0..k); slots past the
-// number of non-empty keys are written as 0.  With kth non-null, thread 0
-// also writes the smallest selected key there (0 if fewer than k keys).
-template <int KPT>
-__device__ void block_select(const uint64_t (&key)[KPT], int k, uint64_t *out, SelectShared &sh,
-                             uint64_t *kth = nullptr) {
+// Radix select, 8 bits per pass from the top, over the keys get(0 .. count)
+// (0 = empty), read again on every pass: writes the min(k, non-empty count)
+// largest, in no particular order, to out[] and zeros to the rest of out[0..k).
+template <class Get>
+__device__ void block_select_stream(Get get, int count, int k, uint64_t *out, SelectShared &sh) {
     const int t = (int)threadIdx.x, nth = (int)blockDim.x;
-    // number of non-empty keys
+    const int rounds = (count + nth - 1) / nth;  // same trip count for every lane (ballots)
     if (t == 0) {
         sh.count = 0;
         sh.prefix = 0;
@@ -77,26 +128,27 @@ __device__ void block_select(const uint64_t (&key)[KPT], int k, uint64_t *out, S
     }
     __syncthreads();
     int mine = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) mine += key[j] != 0;
+    for (int r = 0; r < rounds; ++r) {
+        const int i = r * nth + t;
+        mine += i < count && get(i) != 0;
+    }
     if (mine) atomicAdd(&sh.count, mine);
     __syncthreads();
     const int avail = sh.count;
     if (t == 0) sh.need = min(k, avail);
     __syncthreads();
-    // Narrow the prefix of the need-th largest key, 8 bits at a time.
     for (int shift = 56; shift >= 0 && sh.need > 0 && !sh.done; shift -= 8) {
         for (int b = t; b < 256; b += nth) sh.hist[b] = 0;
         __syncthreads();
         const uint64_t pre = sh.prefix;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            const uint64_t kk = key[j];
+        for (int r = 0; r < rounds; ++r) {
+            const int i = r * nth + t;
+            const uint64_t kk = i < count ? get(i) : 0ull;
             const bool match = kk != 0 && (shift == 56 || (kk >> (shift + 8)) == (pre >> (shift + 8)));
             hist_add(sh.hist, match, (uint32_t)(kk >> shift) & 255u);
         }
         __syncthreads();
-        if (t < 64) {  // one wave: suffix sums over the 256 bins (4 per lane, from the top)
+        if (t < kWave) {  // suffix sums over the 256 bins, 4 per lane from the top
             const int b0 = 255 - 4 * t;
             uint32_t c[4], s = 0;
 #pragma unroll
@@ -104,14 +156,13 @@ __device__ void block_select(const uint64_t (&key)[KPT], int k, uint64_t *out, S
                 c[i] = sh.hist[b0 - i];
                 s += c[i];
             }
-            // inclusive scan of the lane totals over lanes 0..63 (bins from the top)
             uint32_t incl = s;
 #pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t o = __shfl_up(incl, d, 64);
+            for (int d = 1; d < kWave; d <<= 1) {
+                const uint32_t o = __shfl_up(incl, d, kWave);
                 if (t >= d) incl += o;
             }
-            uint32_t run = incl - s;  // keys in bins above b0
+            uint32_t run = incl - s;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 sh.above[b0 - i] = run;
@@ -126,59 +177,85 @@ __device__ void block_select(const uint64_t (&key)[KPT], int k, uint64_t *out, S
                 sh.prefix = pre | ((uint64_t)t << shift);
                 sh.shift = shift;
                 sh.need = need - (int)a;
-                if ((int)h == need - (int)a) sh.done = 1;  // every key of the bin is needed
+                if ((int)h == need - (int)a) sh.done = 1;
             }
         }
         __syncthreads();
     }
-    // Compact: keys whose top (64 - shift) bits are >= the prefix's (exactly
-    // min(k, avail) of them).
     const uint64_t pre = sh.prefix;
     const int shift = sh.shift;
-    if (t == 0) {
-        sh.count = 0;
-        sh.minkey = ~0ull;
-    }
+    if (t == 0) sh.count = 0;
     __syncthreads();
     const int total = min(k, avail);
-    uint64_t mn = ~0ull;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const uint64_t kk = key[j];
-        const bool sel = kk != 0 && (shift >= 64 || (kk >> shift) >= (pre >> shift));
-        if (sel) {
+    for (int r = 0; r < rounds; ++r) {
+        const int i = r * nth + t;
+        const uint64_t kk = i < count ? get(i) : 0ull;
+        if (kk != 0 && (shift >= 64 || (kk >> shift) >= (pre >> shift))) {
             const int slot = atomicAdd(&sh.count, 1);
             if (slot < total) out[slot] = kk;
-            mn = kk < mn ? kk : mn;
         }
     }
-    if (kth && mn != ~0ull) atomicMin((unsigned long long *)&sh.minkey, (unsigned long long)mn);
     for (int i = total + t; i < k; i += nth) out[i] = 0;
     __syncthreads();
-    if (kth && t == 0) *kth = total == k ? sh.minkey : 0ull;
 }
 
-// Pass 1: workgroup g selects the top k of values [g * chunk, (g + 1) * chunk).
-template <int KPT>
-__global__ __launch_bounds__(kTopkBlock1) void k_topk_chunks(const float *__restrict__ v, int n, int k,
-                                                             uint64_t *__restrict__ lists,
-                                                             uint64_t *__restrict__ kth) {
+// 2. Keys >= T of each chunk onto the candidate list.  A chunk with more than
+// k of them (ties, sorted input) contributes only its own top k, so the list
+// holds at most nchunks * k <= kTopkCap keys.
+__global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restrict__ v, int n, int k, int chunk,
+                                                            int nchunks, TopkScratch sc) {
+    __shared__ uint64_t mk[kTopkMaxChunks];
+    __shared__ uint64_t bound;
+    __shared__ uint32_t local, gbase;
     __shared__ SelectShared sh;
-    const int chunk = KPT * kTopkBlock1;
-    const long long base = (long long)blockIdx.x * chunk;
-    uint64_t key[KPT];
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const long long i = base + (long long)j * kTopkBlock1 + threadIdx.x;
-        key[j] = i < n ? topk_key(v[i], (uint32_t)i) : 0ull;
+    __shared__ uint64_t best[kTopkMaxK];
+    const int t = (int)threadIdx.x;
+    if (t < nchunks) mk[t] = sc.maxkey[t];
+    if (t == 0) {
+        bound = 0ull;  // fewer than k chunks: no bound
+        local = 0u;
     }
-    block_select<KPT>(key, k, lists + (size_t)blockIdx.x * k, sh, kth + blockIdx.x);
-}
-
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, mask, kWave);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), mask, kWave);
-    return ((uint64_t)hi << 32) | lo;
+    __syncthreads();
+    if (t < nchunks) {
+        const uint64_t me = mk[t];
+        int rank = 0;
+        for (int j = 0; j < nchunks; ++j) rank += mk[j] > me;
+        if (rank == k - 1) bound = me;  // the maxima are distinct keys: one thread
+    }
+    __syncthreads();
+    const uint64_t T = bound;
+    const int base = (int)blockIdx.x * chunk;
+    const int len = min(n - base, chunk);
+    // Count, reserve, write (the chunk is L2-resident after the first sweep).
+    uint32_t mine = 0;
+    for (int i = t; i < len; i += kTopkBlock) mine += topk_key(v[base + i], (uint32_t)(base + i)) >= T;
+    if (mine) atomicAdd(&local, mine);
+    __syncthreads();
+    const uint32_t found = local;
+    __syncthreads();  // every thread has read local before it is reset
+    if (found > (uint32_t)k) {
+        block_select_stream(
+            [&](int i) {
+                const uint64_t key = topk_key(v[base + i], (uint32_t)(base + i));
+                return key >= T ? key : 0ull;
+            },
+            len, k, best, sh);
+        if (t == 0) gbase = atomicAdd(sc.count, (uint32_t)k);
+        __syncthreads();
+        if (t < k) sc.cand[gbase + t] = best[t];
+        return;
+    }
+    if (t == 0) {
+        gbase = found ? atomicAdd(sc.count, found) : 0u;
+        local = 0u;
+    }
+    __syncthreads();
+    if (!mine) return;
+    uint32_t off = gbase + atomicAdd(&local, mine);
+    for (int i = t; i < len; i += kTopkBlock) {
+        const uint64_t key = topk_key(v[base + i], (uint32_t)(base + i));
+        if (key >= T) sc.cand[off++] = key;
+    }
 }
 
 // Sort one key per lane descending across the 64 lanes (bitonic).
@@ -196,78 +273,65 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, int lane) {
     return key;
 }
 
-// Pass 2: one workgroup selects the top k of the nchunks x k candidates and
-// writes them in rank order.  A chunk's k-th key is a lower bound of the
-// overall k-th key (that chunk alone holds k keys at or above it), so every
-// candidate below the largest such bound is dropped before the selection.
-__global__ __launch_bounds__(kTopkBlock2) void k_topk_final(const uint64_t *__restrict__ lists,
-                                                            const uint64_t *__restrict__ kth, int nchunks, int k,
-                                                            const float *__restrict__ v, int32_t *__restrict__ idx,
-                                                            float *__restrict__ val) {
-    constexpr int KPT = kTopkMaxChunks * kTopkMaxK / kTopkBlock2;  // 16
+__device__ __forceinline__ void topk_emit(const float *v, uint64_t key, int rank, int32_t *idx, float *val) {
+    const uint32_t id = ~(uint32_t)key;
+    idx[rank] = (int32_t)id;
+    val[rank] = v[id];  // the original bits (keeps -0.0 and NaN payloads)
+}
+
+// 3. The top k of the candidates (k <= count <= nchunks * k).
+__global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__restrict__ v, int k, TopkScratch sc,
+                                                               int32_t *__restrict__ idx, float *__restrict__ val) {
+    __shared__ uint64_t keys[kTopkSelBlock];
     __shared__ SelectShared sh;
     __shared__ uint64_t best[kTopkMaxK];
-    __shared__ uint64_t bound;
-    const int ncand = nchunks * k;
-    uint64_t key[KPT];
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const int i = j * kTopkBlock2 + (int)threadIdx.x;
-        key[j] = i < ncand ? lists[i] : 0ull;
-    }
-    if (threadIdx.x == 0) bound = 0ull;
-    __syncthreads();
-    if ((int)threadIdx.x < nchunks) atomicMax((unsigned long long *)&bound, (unsigned long long)kth[threadIdx.x]);
-    __syncthreads();
-    const uint64_t lb = bound;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) key[j] = key[j] >= lb ? key[j] : 0ull;
-    block_select<KPT>(key, k, best, sh);
-    if (threadIdx.x < kWave) {
-        const int lane = (int)threadIdx.x;
-        const uint64_t s = wave_sort_desc(lane < k ? best[lane] : 0ull, lane);
-        if (lane < k) {
-            const uint32_t id = ~(uint32_t)s;
-            idx[lane] = (int32_t)id;
-            val[lane] = v[id];  // the original bits (keeps -0.0 and NaN payloads)
+    const int t = (int)threadIdx.x;
+    const int total = (int)*sc.count;
+    if (total <= kTopkSelBlock) {
+        const uint64_t me = t < total ? sc.cand[t] : 0ull;
+        keys[t] = me;
+        __syncthreads();
+        if (t < total) {
+            int rank = 0;
+            for (int j = 0; j < total; ++j) rank += keys[j] > me;
+            if (rank < k) topk_emit(v, me, rank, idx, val);
         }
+        return;
+    }
+    const uint64_t *cand = sc.cand;
+    block_select_stream([&](int i) { return cand[i]; }, total, k, best, sh);
+    if (t < kWave) {
+        const uint64_t s = wave_sort_desc(t < k ? best[t] : 0ull, t);
+        if (t < k) topk_emit(v, s, t, idx, val);
     }
 }
 
-// Values per pass-1 workgroup: 1024 for the vocab (243 chunks), doubled until
-// the chunks fit pass 2.
-static int topk_kpt(int n) {
-    for (int kpt = 4; kpt <= 64; kpt *= 2)
-        if ((n + kpt * kTopkBlock1 - 1) / (kpt * kTopkBlock1) <= kTopkMaxChunks) return kpt;
+// Values per chunk workgroup: 1024 for the vocab (243 chunks), doubled until
+// the chunk count fits.
+static int topk_chunk(int n) {
+    for (int c = 1024; c <= (1 << 16); c *= 2)
+        if ((n + c - 1) / c <= kTopkMaxChunks) return c;
     return 0;
 }
 
-int topk_max_n() { return 64 * kTopkBlock1 * kTopkMaxChunks; }
+int topk_max_n() { return (1 << 16) * kTopkMaxChunks; }
 
 size_t topk_scratch_bytes(int n) {
-    const int kpt = topk_kpt(n);
-    if (!kpt) return 0;
-    const int chunks = (n + kpt * kTopkBlock1 - 1) / (kpt * kTopkBlock1);
-    return (size_t)chunks * (kTopkMaxK + 1) * sizeof(uint64_t);  // lists, then one k-th key per chunk
+    if (!topk_chunk(n)) return 0;
+    return (size_t)(kTopkMaxChunks + 1 + kTopkCap) * sizeof(uint64_t);
 }
 
 hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, void *scratch, hipStream_t s) {
-    const int kpt = topk_kpt(n);
-    if (!kpt) return hipErrorInvalidValue;
-    const int chunks = (n + kpt * kTopkBlock1 - 1) / (kpt * kTopkBlock1);
-    uint64_t *lists = (uint64_t *)scratch;
-    uint64_t *kth = lists + (size_t)chunks * kTopkMaxK;
-    const dim3 g(chunks), b(kTopkBlock1);
-    switch (kpt) {
-        case 4: hipLaunchKernelGGL((k_topk_chunks<4>), g, b, 0, s, v, n, k, lists, kth); break;
-        case 8: hipLaunchKernelGGL((k_topk_chunks<8>), g, b, 0, s, v, n, k, lists, kth); break;
-        case 16: hipLaunchKernelGGL((k_topk_chunks<16>), g, b, 0, s, v, n, k, lists, kth); break;
-        case 32: hipLaunchKernelGGL((k_topk_chunks<32>), g, b, 0, s, v, n, k, lists, kth); break;
-        default: hipLaunchKernelGGL((k_topk_chunks<64>), g, b, 0, s, v, n, k, lists, kth); break;
-    }
+    const int chunk = topk_chunk(n);
+    if (!chunk) return hipErrorInvalidValue;
+    const int nchunks = (n + chunk - 1) / chunk;
+    const TopkScratch sc = topk_scratch(scratch);
+    hipLaunchKernelGGL(k_topk_chunk_max, dim3(nchunks), dim3(kTopkBlock), 0, s, v, n, chunk, sc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(kTopkBlock2), 0, s, lists, kth, chunks, k, v, idx, val);
+    hipLaunchKernelGGL(k_topk_filter, dim3(nchunks), dim3(kTopkBlock), 0, s, v, n, k, chunk, nchunks, sc);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kTopkSelBlock), 0, s, v, k, sc, idx, val);
     return hipGetLastError();
 }
 

@@ -51,6 +51,28 @@ def test_topk_ties_zeros_nan_inf(m27q, ora, dev):
     assert list(idx) == [1, 2, 0, 3]
 
 
+@pytest.mark.parametrize("case,k", [("equal", 8), ("equal", 64), ("descending", 64), ("ascending", 33)])
+def test_topk_candidate_paths(m27q, ora, dev, case, k):
+    """The filter's and the select's paths at the vocab size.  The bound is the
+    k-th largest chunk maximum (chunks of 1024): with all values equal, k = 8
+    leaves 7 full chunks above it, each reduced to its own top 8 (57 candidates,
+    ranked directly), and k = 64 leaves 63, reduced to 63 x 64 + 1 = 4033
+    candidates (radix select over the list); sorted inputs put all the
+    candidates in a few chunks."""
+    n = 248320
+    if case == "equal":
+        v = np.full(n, 0.5, np.float32)
+    else:
+        v = np.linspace(-3.0, 3.0, n, dtype=np.float32)
+        if case == "descending":
+            v = v[::-1].copy()
+    say("topk path", case, k)
+    idx, val = run_topk(m27q, dev, v, k)
+    oi, ov = ora.topk(v, k)
+    assert np.array_equal(idx, oi)
+    assert np.array_equal(val.view(np.uint32), ov.view(np.uint32))
+
+
 def test_vocab_scoring_full_size(m27q, ora, dev):
     """Config 5 scoring: Q6_K 248320 x 5120 LM head GEMV of a N(0,1) hidden state,
     exact top-64 on the GPU logits vs the oracle on the same logits, and a row
