@@ -145,7 +145,15 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, swiglu, cfg, p, stream));
 }
 
-// Small-M products on int8 MFMA for TILED weights (m27q_mma.hip).
+// Small-M products for TILED weights: up to kMtMaxM tokens on the GEMV
+// streaming structure when their activations fit the LDS budget
+// (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).
+#ifndef M27Q_MT_MAXM
+#define M27Q_MT_MAXM 4
+#endif
+constexpr int kMtMaxM = M27Q_MT_MAXM;
+constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU
+
 m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
                               const float *const *res, hipStream_t stream) {
     for (int i = 0; i < n; ++i) {
@@ -161,7 +169,8 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
     p.K = k_of(&ws[0]);
     p.M = M;
-    if (matmul_mfma_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(ws[0].ggml_type, p.upr, M) <= kMtLdsBudget;
+    if (!few && matmul_mfma_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
     const ActView a = act_view(xq, M, p.K);
     p.xq = a.q;
     p.xd = a.d;
@@ -173,7 +182,8 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
         p.res[i] = res[i];
         p.rc[i] = (int)ws[i].row_count;
     }
-    return hip_status(launch_matmul_mfma(ws[0].ggml_type, p, stream));
+    return hip_status(few ? launch_matmul_mt(ws[0].ggml_type, p, stream)
+                          : launch_matmul_mfma(ws[0].ggml_type, p, stream));
 }
 
 }  // namespace

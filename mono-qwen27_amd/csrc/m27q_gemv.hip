@@ -119,42 +119,6 @@ __device__ __forceinline__ int stage_span(int Kp) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Weight fragments of one unit for the TPW tiles of every matrix.
-template <class T, int LAYOUT, int NM, int TPW>
-struct UnitStream {
-    const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
-    int i, c, rb;
-    typename T::Lane L;
-
-    __device__ UnitStream(const uint8_t *const *W, int tile0, int ntiles, int rc, int rb_, int upr, int lane)
-        : i(lane >> 3), c(lane & 7), rb(rb_), L(lane & 7) {
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int t = 0; t < TPW; ++t) {
-                const int tile = min(tile0 + t, ntiles - 1);  // past the end: reread the last tile
-                if constexpr (LAYOUT == M27Q_LAYOUT_TILED) {
-                    base[m][t] = W[m] + (size_t)tile * upr * T::kUnitBytes;
-                } else {
-                    const int row = min(tile * kTileRows + i, rc - 1);
-                    base[m][t] = W[m] + (size_t)row * rb_ * T::kBlockBytes;
-                }
-            }
-    }
-
-    __device__ void load(typename T::Frag (&f)[NM][TPW], int u) const {
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int t = 0; t < TPW; ++t) {
-                if constexpr (LAYOUT == M27Q_LAYOUT_TILED)
-                    f[m][t] = T::load_tiled(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
-                else
-                    f[m][t] = T::load_gguf(base[m][t], u, rb, c, L);
-            }
-    }
-};
-
 template <class T, int NM, int TPW>
 __device__ __forceinline__ void compute_unit(const typename T::Frag (&f)[NM][TPW], const ActLds &act, int u,
                                              const typename T::Lane &L, float (&acc)[NM][TPW]) {

@@ -1,0 +1,240 @@
+// m27q_gemv_mt.hip -- small-M products Y[M][N] = X[M][K] W[N][K]^T for a few
+// tokens on the M = 1 GEMV's streaming structure.
+//
+// The weights are streamed exactly as by the M = 1 kernel (TILED layout, 8-row
+// tiles, K split over KS waves, 16-byte loads of one unit per lane, double
+// buffered and unconditional), and every loaded fragment is applied to MT
+// activation rows staged in LDS: the weight unpacking is shared by the tokens,
+// each token adds its own integer dots and scale terms, and no lane works on a
+// padding token unless M is not a multiple of MT.  The 16 x 16 MFMA tile, by
+// contrast, spends the same scale arithmetic on 16 token columns whatever M
+// is.  Measured on the Qwen-27B layer: 66 us against 115 us at M = 2, 103
+// against 118 at M = 4; at M = 8 the per-token dots make it no faster than
+// the MFMA kernel, which keeps M > 4.
+// No reference counterpart: the reference runs prefill and decode one token at
+// a time (src/mono27b_chat.cpp:399-403).
+#include <algorithm>
+
+#include "m27q_internal.h"
+#include "m27q_types.h"
+
+namespace m27q {
+
+template <class T, class C, int MT>
+__global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, int m0) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
+    constexpr int NR = TPW * kTileRows;  // rows per workgroup
+    const int lane = (int)(threadIdx.x & 63), i = lane >> 3, c = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int ks = wave % KS, tg = wave / KS;
+    const int nth = C::NW * kWave;
+
+    int mi = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMulti; ++k)
+        if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) mi = k;
+    const int rc = p.rc[mi];
+    const int tile0 = ((int)blockIdx.x - p.wg_start[mi]) * TPW;
+    const int ntiles = (rc + kTileRows - 1) / kTileRows;
+    const int U = p.upr / KS, rem = p.upr % KS;
+    const int ub = ks * U + min(ks, rem);
+    const int nu = U + (ks < rem ? 1 : 0);
+
+    // First unit of weights before the staging, so their latencies overlap.
+    const uint8_t *W[1] = {p.W[mi]};
+    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT> ws(W, tile0 + tg * WT, ntiles, rc, 0, p.upr, lane);
+    typename T::Frag fa[1][WT], fb[1][WT];
+    ws.load(fa, min(ub, p.upr - 1));
+
+    // Activations of tokens m0 .. m0 + MT: codes [MT][Kp] | d [MT][Kp/32] |
+    // aux [MT][Kp/32], zero past K and past M.  Loads go out 4 per thread
+    // before their stores.
+    const int Kp = p.upr * T::kUnitElems, gp = Kp / 32, ng = p.K / 32;
+    const int nq = Kp / 16;
+    int8_t *xc = (int8_t *)smem;
+    float *xd = (float *)(smem + (size_t)MT * Kp);
+    uint32_t *xs = (uint32_t *)(xd + MT * gp);
+    for (int j0 = (int)threadIdx.x; j0 < MT * nq; j0 += 4 * nth) {
+        uint4 v[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = j0 + b * nth, tok = j / nq, q16 = j % nq;
+            const bool in = j < MT * nq && m0 + tok < p.M && 16 * q16 < p.K;
+            const size_t src = in ? (size_t)(m0 + tok) * p.K + 16 * q16 : 0;
+            v[b] = *(const uint4 *)(p.xq + src);
+            if (!in) v[b] = make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = j0 + b * nth;
+            if (j < MT * nq) ((uint4 *)xc)[j] = v[b];
+        }
+    }
+    for (int j0 = (int)threadIdx.x; j0 < MT * gp; j0 += 4 * nth) {
+        float d[4];
+        uint32_t s[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = j0 + b * nth, tok = j / gp, g = j % gp;
+            const bool in = j < MT * gp && m0 + tok < p.M && g < ng;
+            const size_t src = in ? (size_t)(m0 + tok) * ng + g : 0;
+            d[b] = p.xd[src];
+            s[b] = p.xs[src];
+            if (!in) {
+                d[b] = 0.f;
+                s[b] = 0u;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = j0 + b * nth;
+            if (j < MT * gp) {
+                xd[j] = d[b];
+                xs[j] = T::stage_aux(d[b], s[b]);
+            }
+        }
+    }
+    float *red = (float *)(xs + MT * gp);  // [MT][KS][NR]
+    __syncthreads();
+
+    float acc[MT][WT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < WT; ++t) acc[mt][t] = 0.f;
+    auto compute = [&](const typename T::Frag (&f)[1][WT], int u) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const ActLds act{xc + (size_t)mt * Kp, xd + mt * gp, xs + mt * gp};
+            const typename T::AFrag a = T::load_act(act, u, ws.L);
+#pragma unroll
+            for (int t = 0; t < WT; ++t) acc[mt][t] += T::dot(f[0][t], a, ws.L);
+        }
+    };
+    int k = 0;
+    for (; k + 2 < nu; k += 2) {
+        ws.load(fb, ub + k + 1);
+        compute(fa, ub + k);
+        ws.load(fa, ub + k + 2);
+        compute(fb, ub + k + 1);
+    }
+    if (k + 1 < nu) {
+        ws.load(fb, ub + k + 1);
+        compute(fa, ub + k);
+        compute(fb, ub + k + 1);
+    } else if (k < nu) {
+        compute(fa, ub + k);
+    }
+
+    // Row partials of this wave's K slice -> LDS; then one thread per (token,
+    // row) adds the KS partials in a fixed order.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < WT; ++t) {
+            const float r = sum8(acc[mt][t]);
+            if (c == 0) red[(mt * KS + ks) * NR + (tg * WT + t) * kTileRows + i] = r;
+        }
+    __syncthreads();
+    for (int idx = (int)threadIdx.x; idx < MT * NR; idx += nth) {
+        const int mt = idx / NR, rr = idx % NR, row = tile0 * kTileRows + rr, tok = m0 + mt;
+        float v = red[mt * KS * NR + rr];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) v += red[(mt * KS + w) * NR + rr];
+        if (row < rc && tok < p.M) {
+            const size_t o = (size_t)tok * rc + row;
+            p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
+        }
+    }
+}
+
+template <class T, class C, int MT>
+static size_t mt_lds(int upr) {
+    const size_t Kp = (size_t)upr * T::kUnitElems;
+    return MT * (Kp + Kp / 4) + (size_t)MT * C::KS * C::TPW * kTileRows * sizeof(float);
+}
+
+template <class T, class C, int MT>
+static hipError_t launch_mt_cfg(MatmulMultiParams p, hipStream_t s) {
+    int total = 0;
+    for (int i = 0; i < p.nmat; ++i) {
+        p.wg_start[i] = total;
+        total += ((p.rc[i] + kTileRows - 1) / kTileRows + C::TPW - 1) / C::TPW;
+    }
+    p.wg_start[p.nmat] = total;
+    const size_t lds = mt_lds<T, C, MT>(p.upr);
+    for (int m0 = 0; m0 < p.M; m0 += MT) {
+        hipLaunchKernelGGL((k_gemv_mt<T, C, MT>), dim3(total), dim3(kWave * C::NW), lds, s, p, m0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Launch shape, from sweeps of the Qwen-27B layer at M = 2 and 4: (8, 4, 4)
+// for q/k/v (8192 rows of 20 units), (8, 1, 1) for o (24 units) and down (68
+// units), (4, 2, 2) for gate/up (34816 rows).
+static int pick_mt_cfg(long long rows, int upr) {
+    if (upr >= 24) return kCfg81;
+    return rows <= 12288 ? kCfg84 : kCfg42;
+}
+
+template <class T, int MT>
+static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
+#ifdef M27Q_MT_CFG
+    constexpr int forced = M27Q_MT_CFG;
+    const int cfg = forced;
+#else
+    long long rows = 0;
+    for (int i = 0; i < p.nmat; ++i) rows += p.rc[i];
+    const int cfg = pick_mt_cfg(rows, p.upr);
+#endif
+    switch (cfg) {
+        case kCfg81: return launch_mt_cfg<T, Cfg81, MT>(p, s);
+        case kCfg42: return launch_mt_cfg<T, Cfg42, MT>(p, s);
+        case kCfg84: return launch_mt_cfg<T, Cfg84, MT>(p, s);
+        default: return launch_mt_cfg<T, Cfg41, MT>(p, s);
+    }
+}
+
+static int mt_of(int M) { return M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M) {
+    // the largest over the launch shapes the selection can return
+    const int mt = mt_of(M);
+    auto one = [&](auto tag) -> size_t {
+        using T = decltype(tag);
+        switch (mt) {
+            case 2: return std::max({mt_lds<T, Cfg41, 2>(upr), mt_lds<T, Cfg81, 2>(upr), mt_lds<T, Cfg42, 2>(upr), mt_lds<T, Cfg84, 2>(upr)});
+            case 4: return std::max({mt_lds<T, Cfg41, 4>(upr), mt_lds<T, Cfg81, 4>(upr), mt_lds<T, Cfg42, 4>(upr), mt_lds<T, Cfg84, 4>(upr)});
+            default: return std::max({mt_lds<T, Cfg41, 8>(upr), mt_lds<T, Cfg81, 8>(upr), mt_lds<T, Cfg42, 8>(upr), mt_lds<T, Cfg84, 8>(upr)});
+        }
+    };
+    switch (type) {
+        case kQ4_K: return one(Q4K{});
+        case kQ6_K: return one(Q6K{});
+        case kQ8_0: return one(Q80{});
+        default: return 0;
+    }
+}
+
+template <class T>
+static hipError_t launch_mt_m(const MatmulMultiParams &p, hipStream_t s) {
+    switch (mt_of(p.M)) {
+        case 2: return launch_mt_t<T, 2>(p, s);
+        case 4: return launch_mt_t<T, 4>(p, s);
+        default: return launch_mt_t<T, 8>(p, s);
+    }
+}
+
+hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_mt_m<Q4K>(p, s);
+        case kQ6_K: return launch_mt_m<Q6K>(p, s);
+        case kQ8_0: return launch_mt_m<Q80>(p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace m27q

@@ -14,6 +14,10 @@ CASES = [  # type, rows, K, M, layout
     ("Q4_K", 40, 512, 5, 0), ("Q4_K", 40, 512, 64, 1),
     ("Q6_K", 5120, 17408, 16, 1), ("Q6_K", 5120, 17408, 3, 0), ("Q6_K", 24, 768, 9, 1),
     ("Q8_0", 2048, 6144, 16, 1), ("Q8_0", 2048, 6144, 2, 0), ("Q8_0", 13, 160, 7, 1),
+    # few-token GEMV path (M <= 4, TILED): a padding token (M = 3), partial
+    # 8-row tiles, each type
+    ("Q6_K", 5120, 17408, 2, 1), ("Q6_K", 24, 768, 4, 1), ("Q4_K", 40, 512, 3, 1), ("Q8_0", 13, 160, 3, 1),
+    ("Q8_0", 2048, 6144, 4, 1),
 ]
 
 
