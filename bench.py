@@ -221,6 +221,19 @@ def capture(torch, fn):
     return g
 
 
+def replay_times(torch, g, reps):
+    """ms of each replay, from HIP events between consecutive replays."""
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record(s)
+    for i in range(reps):
+        g.replay()
+        ev[i + 1].record(s)
+    ev[-1].synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(reps)]
+
+
 def time_graph(torch, g, reps):
     """Average ms per replay, HIP events on the replay stream."""
     s = torch.cuda.current_stream()
@@ -234,26 +247,45 @@ def time_graph(torch, g, reps):
     return e0.elapsed_time(e1) / reps
 
 
-def cpu_baseline(ora, host, budget_s=12.0):
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(ora, host, budget_s=12.0, single_budget_s=4.0):
     """The oracle's restatement of ggml's CPU path (q8_K activations, q4_K x q8_K /
-    q6_K x q8_K dots), rows split over host threads, on the same layer weights."""
+    q6_K x q8_K dots), rows split over host threads, on the same layer weights;
+    timed at up to 16 threads (the box's CPU share) and at one thread."""
     nthreads = max(1, min(16, os.cpu_count() or 1))
     x = np.random.default_rng(1).standard_normal(17408).astype(np.float32)
     xq = {k: ora.quant_cpu_act(ora.Q4_K, x[:k]) for k in (5120, 6144, 17408)}
     total_bytes = sum(b.nbytes for (_, _, _, b) in host.values())
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        for name, (t, rc, k, blocks) in host.items():
-            ora.gemv_cpu(t, blocks, k // 256, rc, xq[k], nthreads=nthreads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or (reps >= 3 and el * (reps + 1) / reps > budget_s):
-            break
-    sec = el / reps
+
+    def passes(nt, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            for name, (t, rc, k, blocks) in host.items():
+                ora.gemv_cpu(t, blocks, k // 256, rc, xq[k], nthreads=nt)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or (reps >= 1 and el * (reps + 1) / reps > budget):
+                return reps, el
+
+    reps, el = passes(nthreads, budget_s)
+    reps1, el1 = passes(1, single_budget_s)
+    sec, sec1 = el / reps, el1 / reps1
     return {"value": round(total_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": f"{reps} full layer passes (7 matvecs, {total_bytes} weight bytes) in {el:.2f} s, "
-                      f"{sec * 1e6:.0f} us/layer; oracle restatement of ggml q4_K/q6_K x q8_K CPU dots "
-                      f"(not ggml itself: the vendored ref/llama.cpp is empty)"}
+            "single_thread_value": round(total_bytes / sec1 / 1e9, 3),
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "sample": f"{reps} full layer passes (7 matvecs, {total_bytes} weight bytes) in {el:.2f} s at "
+                      f"{nthreads} threads ({sec * 1e6:.0f} us/layer), {reps1} in {el1:.2f} s at 1 thread "
+                      f"({sec1 * 1e6:.0f} us/layer); oracle restatement of ggml q4_K/q6_K x q8_K CPU dots, "
+                      f"AVX2 C (not ggml itself: the vendored ref/llama.cpp is empty)"}
 
 
 def main():
@@ -302,6 +334,7 @@ def main():
     log(f"timing {reps * copies} layer passes")
     ms_cold = time_graph(torch, g_cold, reps) / copies
     ms_warm = time_graph(torch, g_warm, reps) / copies
+    per = np.array(replay_times(torch, g_cold, reps)) / copies * 1e3  # us per layer, one value per replay
 
     # Each product on its own, over the same rotated copies: average launch
     # duration from HIP events on the replay stream.
@@ -346,6 +379,7 @@ def main():
                    "weight_bytes": layer_bytes, "layout": "tiled", "activation": "int8 per-32, fp32 scale",
                    "cold_copies": copies, "graph": True},
         "us_per_layer": round(ms_cold * 1e3, 2),
+        "us_per_layer_p10_median_p90": [round(float(np.percentile(per, q)), 2) for q in (10, 50, 90)],
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "lower_bound_us": round(layer_bytes / HBM_PEAK_GBS / 1e3, 2),
         "x_lower_bound": round(ms_cold * 1e3 / (layer_bytes / HBM_PEAK_GBS / 1e3), 3),
