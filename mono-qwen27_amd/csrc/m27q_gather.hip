@@ -63,6 +63,43 @@ __device__ __forceinline__ float4 cvt_q4k(const Raw &w, int l) {
                        d1 * (float)((q >> (16 + sh)) & 15u) - m1, d1 * (float)((q >> (24 + sh)) & 15u) - m1);
 }
 
+// Q5_K: the Q4_K words plus the 4 qh bytes of the lane's positions.
+__device__ __forceinline__ Raw load_q5k(const GatherParams &p, int r, int b, int l) {
+    const int g = l >> 4, t = 4 * (l & 15), lq = t & 31;
+    Raw w;
+    const uint8_t *hdr, *qs, *qh;
+    if (p.layout == M27Q_LAYOUT_TILED) {
+        const uint8_t *unit = p.W + ((size_t)(r / kTileRows) * p.upr + b) * kQ5KUnit;
+        const int i = r % kTileRows;
+        hdr = unit + 16 * i;
+        qs = unit + 128 + 128 * i;
+        qh = unit + kQ5KTQh + 32 * i;
+    } else {
+        hdr = p.W + ((size_t)r * p.rb + b) * kQ5KBytes;
+        qs = hdr + kQ5KQs;
+        qh = hdr + kQ5KQh;
+    }
+    w.a = *(const uint4 *)hdr;
+    w.b = *(const uint32_t *)(qs + 32 * g + lq);
+    w.c = *(const uint32_t *)(qh + lq);
+    return w;
+}
+__device__ __forceinline__ float4 cvt_q5k(const Raw &w, int l) {
+    const int g = l >> 4, t = 4 * (l & 15), hi = t >> 5, j = 2 * g + hi;
+    int sc, m;
+    scale_min_k4(j, w.a.y, w.a.z, w.a.w, sc, m);
+    const float d1 = f16_bits_to_f32(w.a.x) * (float)sc;
+    const float m1 = f16_bits_to_f32(w.a.x >> 16) * (float)m;
+    const int sh = 4 * hi;
+    float o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t q = ((w.b >> (8 * k + sh)) & 15u) | (((w.c >> (8 * k + j)) & 1u) << 4);
+        o[k] = d1 * (float)q - m1;
+    }
+    return make_float4(o[0], o[1], o[2], o[3]);
+}
+
 __device__ __forceinline__ Raw load_q6k(const GatherParams &p, int r, int b, int l) {
     const int h = l >> 5, r4 = (l & 31) >> 3, lq = 4 * (l & 7);
     const int qlo = 64 * h + 32 * (r4 & 1) + lq, qho = 32 * h + lq, sci = 8 * h + lq / 16 + 2 * r4;
@@ -120,7 +157,7 @@ __device__ __forceinline__ float4 cvt_q80(const Raw &w) {
 constexpr int kGatherCpw = 8;  // chunks per wave in one workgroup column
 
 __device__ __forceinline__ int gather_k(const GatherParams &p) {
-    return p.type == kQ8_0 ? p.rb * 32 : (p.type == kQ4_K || p.type == kQ6_K ? p.rb * 256 : p.rb);
+    return p.type == kQ8_0 ? p.rb * 32 : (p.type == kF16 || p.type == kF32 ? p.rb : p.rb * 256);
 }
 
 // grid.x = output row; workgroup column blockIdx.y covers chunks
@@ -148,6 +185,7 @@ __global__ __launch_bounds__(256) void k_gather(GatherParams p) {
         const int ch = min(c0 + 4 * j, nchunk - 1);  // past the end: reload the last chunk, store nothing
         const int pos = min(ch * 256 + 4 * lane, K - 4);
         if constexpr (TYPE == kQ4_K) w[j] = load_q4k(p, r, ch, lane);
+        else if constexpr (TYPE == kQ5_K) w[j] = load_q5k(p, r, ch, lane);
         else if constexpr (TYPE == kQ6_K) w[j] = load_q6k(p, r, ch, lane);
         else if constexpr (TYPE == kQ8_0) w[j] = load_q80(p, r, pos / 32, pos % 32);  // K % 32 == 0
         else if constexpr (TYPE == kF16) {
@@ -164,6 +202,7 @@ __global__ __launch_bounds__(256) void k_gather(GatherParams p) {
         if (ch >= nchunk || pos >= K) continue;
         float4 v;
         if constexpr (TYPE == kQ4_K) v = cvt_q4k(w[j], lane);
+        else if constexpr (TYPE == kQ5_K) v = cvt_q5k(w[j], lane);
         else if constexpr (TYPE == kQ6_K) v = cvt_q6k(w[j], lane);
         else if constexpr (TYPE == kQ8_0) v = cvt_q80(w[j]);
         else if constexpr (TYPE == kF16)
@@ -176,11 +215,12 @@ __global__ __launch_bounds__(256) void k_gather(GatherParams p) {
 }
 
 hipError_t launch_gather(const GatherParams &p, hipStream_t s) {
-    const int K = p.type == kQ8_0 ? p.rb * 32 : (p.type == kQ4_K || p.type == kQ6_K ? p.rb * 256 : p.rb);
+    const int K = p.type == kQ8_0 ? p.rb * 32 : (is_quant(p.type) ? p.rb * 256 : p.rb);
     const int chunks = (K + 255) / 256;
     const dim3 grid(p.n, (chunks + 4 * kGatherCpw - 1) / (4 * kGatherCpw)), block(256);
     switch (p.type) {
         case kQ4_K: hipLaunchKernelGGL(k_gather<kQ4_K>, grid, block, 0, s, p); break;
+        case kQ5_K: hipLaunchKernelGGL(k_gather<kQ5_K>, grid, block, 0, s, p); break;
         case kQ6_K: hipLaunchKernelGGL(k_gather<kQ6_K>, grid, block, 0, s, p); break;
         case kQ8_0: hipLaunchKernelGGL(k_gather<kQ8_0>, grid, block, 0, s, p); break;
         case kF16: hipLaunchKernelGGL(k_gather<kF16>, grid, block, 0, s, p); break;

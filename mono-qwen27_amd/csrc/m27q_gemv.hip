@@ -26,10 +26,12 @@
 // simpler one-wave-per-tile mapping: they are the fallback, not the hot path.
 //
 // Replaces k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a / k_q80_mv_q8_dp4a
-// (exec:320-364, :631-645, :535-580), k_q4k_q4k_swiglu_dp4a (exec:369-417),
+// (exec:320-364, :631-645, :535-580), k_q5k_mv_q8 (exec:497-531),
+// k_q4k_q4k_swiglu_dp4a (exec:369-417),
 // k_quant_q8_1 in front of them (exec:84-107, launched by l_quant_q8_n
 // :2022-2030) and the fp32 fallbacks k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv
-// / k_f32_mv (exec:920-951, :1053-1072, :1076-1096, :899-916, :1100-1114).
+// / k_f32_mv / k_q5k_mv (exec:920-951, :1053-1072, :1076-1096, :899-916,
+// :1100-1114, :953-985).
 #include "m27q_gemv_cfg.h"
 #include "m27q_internal.h"
 #include "m27q_types.h"
@@ -423,6 +425,7 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
 size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg) {
     switch (type) {
         case kQ4_K: return lds_for<Q4K>(upr, swiglu, cfg);
+        case kQ5_K: return lds_for<Q5K>(upr, swiglu, cfg);
         case kQ6_K: return lds_for<Q6K>(upr, swiglu, cfg);
         case kQ8_0: return lds_for<Q80>(upr, swiglu, cfg);
         default: return 0;
@@ -442,6 +445,7 @@ int gemv_q8_tiles_per_wg(int cfg) {
 hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, int cfg, const GemvParams &p, hipStream_t s) {
     switch (type) {
         case kQ4_K: return launch_q8_x<Q4K>(p, layout, swiglu, cfg, s);
+        case kQ5_K: return launch_q8_x<Q5K>(p, layout, swiglu, cfg, s);
         case kQ6_K: return launch_q8_x<Q6K>(p, layout, swiglu, cfg, s);
         case kQ8_0: return launch_q8_x<Q80>(p, layout, swiglu, cfg, s);
         default: return hipErrorInvalidValue;
@@ -470,6 +474,7 @@ static hipError_t launch_f32_l(const GemvParams &p, int layout, int grid, hipStr
 hipError_t launch_gemv_f32(uint32_t type, int layout, const GemvParams &p, int grid, hipStream_t s) {
     switch (type) {
         case kQ4_K: return launch_f32_l<Q4K>(p, layout, grid, s);
+        case kQ5_K: return launch_f32_l<Q5K>(p, layout, grid, s);
         case kQ6_K: return launch_f32_l<Q6K>(p, layout, grid, s);
         case kQ8_0: return launch_f32_l<Q80>(p, layout, grid, s);
         case kF16:

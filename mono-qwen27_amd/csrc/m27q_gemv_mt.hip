@@ -213,6 +213,7 @@ size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M) {
     };
     switch (type) {
         case kQ4_K: return one(Q4K{});
+        case kQ5_K: return one(Q5K{});
         case kQ6_K: return one(Q6K{});
         case kQ8_0: return one(Q80{});
         default: return 0;
@@ -231,6 +232,7 @@ static hipError_t launch_mt_m(const MatmulMultiParams &p, hipStream_t s) {
 hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
         case kQ4_K: return launch_mt_m<Q4K>(p, s);
+        case kQ5_K: return launch_mt_m<Q5K>(p, s);
         case kQ6_K: return launch_mt_m<Q6K>(p, s);
         case kQ8_0: return launch_mt_m<Q80>(p, s);
         default: return hipErrorInvalidValue;

@@ -24,6 +24,19 @@ void move_q4k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
     }
 }
 
+void move_q5k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
+    uint8_t *hdr = unit + 16 * i, *qs = unit + 128 + 128 * i, *qh = unit + kQ5KTQh + 32 * i;
+    if (to_tiled) {
+        std::memcpy(hdr, blk, kQ4KHdr);
+        std::memcpy(qh, blk + kQ5KQh, 32);
+        std::memcpy(qs, blk + kQ5KQs, 128);
+    } else {
+        std::memcpy(blk, hdr, kQ4KHdr);
+        std::memcpy(blk + kQ5KQh, qh, 32);
+        std::memcpy(blk + kQ5KQs, qs, 128);
+    }
+}
+
 void move_q6k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
     struct Piece { int tiled, gguf, len; };
     const Piece pieces[4] = {
@@ -71,6 +84,7 @@ m27q_status convert(uint32_t type, uint32_t rb, uint32_t rc, const void *src, vo
             } else {
                 uint8_t *unit = tiled + ((size_t)t * upr + b) * ub;
                 if (type == kQ4_K) move_q4k(unit, i, blk, to_tiled);
+                else if (type == kQ5_K) move_q5k(unit, i, blk, to_tiled);
                 else move_q6k(unit, i, blk, to_tiled);
             }
         }

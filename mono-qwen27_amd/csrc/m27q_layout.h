@@ -2,7 +2,7 @@
 //
 // Shared by the host packer (m27q_layout.cpp) and the gfx950 kernels.  The
 // GGUF block byte layouts are fixed by the file format (the reference's
-// BlockQ4K / BlockQ6K / BlockQ8 structs, exec:18-28, :57-62, hold the same
+// BlockQ4K / BlockQ5K / BlockQ6K / BlockQ8 structs, exec:18-36, :57-62, hold the same
 // bytes); the TILED layout is this library's own.
 #pragma once
 
@@ -12,15 +12,17 @@
 namespace m27q {
 
 // ggml type ids (include/mono27b_gguf.h:27-43).
-constexpr uint32_t kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
+constexpr uint32_t kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14;
 
 // GGUF block sizes in bytes / weights (src/mono27b_gguf.cpp:167-195).
 constexpr int kQ4KBytes = 144;   // f16 d, f16 dmin, u8 scales[12], u8 qs[128]
+constexpr int kQ5KBytes = 176;   // f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
 constexpr int kQ6KBytes = 210;   // u8 ql[128], u8 qh[64], i8 scales[16], f16 d
 constexpr int kQ80Bytes = 34;    // f16 d, i8 qs[32]
 
 // Byte offsets inside one GGUF block.
 constexpr int kQ4KHdr = 16;      // d, dmin, scales: bytes [0, 16)
+constexpr int kQ5KQh = 16, kQ5KQs = 48;
 constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 
 // ---------------------------------------------------------------- TILED --
@@ -32,6 +34,10 @@ constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 //  Q4_K  unit = one block column                          1152 B
 //        [0, 128)      8 x 16 B headers (d, dmin, scales[12])  row i at 16 i
 //        [128, 1152)   8 x 128 B qs                            row i at 128 + 128 i
+//  Q5_K  unit = one block column                          1408 B
+//        [0, 128)      8 x 16 B headers (d, dmin, scales[12])  row i at 16 i
+//        [128, 1152)   8 x 128 B qs                            row i at 128 + 128 i
+//        [1152, 1408)  8 x 32 B qh                             row i at 1152 + 32 i
 //  Q6_K  unit = one block column                          1680 B
 //        [0, 1024)     8 x 128 B ql                            row i at 128 i
 //        [1024, 1536)  8 x 64 B qh                             row i at 1024 + 64 i
@@ -49,6 +55,8 @@ constexpr int kLanesPerRow = 8;                    // GEMV: 8 lanes x 16 B per r
 constexpr int kWavesPerWG = 4;                     // GEMV workgroup = 4 waves ...
 constexpr int kRowsPerWG = kWavesPerWG * kTileRows;  // ... = 32 output rows
 constexpr int kQ4KUnit = kTileRows * kQ4KBytes;      // 1152
+constexpr int kQ5KUnit = kTileRows * kQ5KBytes;      // 1408
+constexpr int kQ5KTQh = 1152;
 constexpr int kQ6KUnit = kTileRows * kQ6KBytes;      // 1680
 constexpr int kQ80UnitBlocks = 4;
 constexpr int kQ80Unit = kTileRows * kQ80UnitBlocks * kQ80Bytes;  // 1088
@@ -56,12 +64,13 @@ constexpr int kQ80Unit = kTileRows * kQ80UnitBlocks * kQ80Bytes;  // 1088
 constexpr int kQ6KTQl = 0, kQ6KTQh = 1024, kQ6KTSc = 1536, kQ6KTD = 1664;
 constexpr int kQ80TD = 1024;
 
-static_assert(kQ4KUnit % 16 == 0 && kQ6KUnit % 16 == 0 && kQ80Unit % 16 == 0,
+static_assert(kQ4KUnit % 16 == 0 && kQ5KUnit % 16 == 0 && kQ6KUnit % 16 == 0 && kQ80Unit % 16 == 0,
               "every tiled unit keeps 16-byte alignment");
 
 inline int block_bytes(uint32_t type) {
     switch (type) {
         case kQ4_K: return kQ4KBytes;
+        case kQ5_K: return kQ5KBytes;
         case kQ6_K: return kQ6KBytes;
         case kQ8_0: return kQ80Bytes;
         case kF16: return 2;
@@ -72,14 +81,14 @@ inline int block_bytes(uint32_t type) {
 
 inline int block_elems(uint32_t type) {
     switch (type) {
-        case kQ4_K: case kQ6_K: return 256;
+        case kQ4_K: case kQ5_K: case kQ6_K: return 256;
         case kQ8_0: return 32;
         case kF16: case kF32: return 1;
         default: return 0;
     }
 }
 
-inline bool is_quant(uint32_t type) { return type == kQ4_K || type == kQ6_K || type == kQ8_0; }
+inline bool is_quant(uint32_t type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0; }
 
 inline int tiles_of(uint32_t rows) { return (int)((rows + kTileRows - 1) / kTileRows); }
 
@@ -90,6 +99,7 @@ inline int units_per_row(uint32_t type, uint32_t rb) {
 inline int unit_bytes(uint32_t type) {
     switch (type) {
         case kQ4_K: return kQ4KUnit;
+        case kQ5_K: return kQ5KUnit;
         case kQ6_K: return kQ6KUnit;
         case kQ8_0: return kQ80Unit;
         default: return 0;

@@ -116,6 +116,7 @@ static hipError_t launch_l(const MatmulParams &p, int layout, hipStream_t s) {
 hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s) {
     switch (type) {
         case kQ4_K: return launch_l<Q4K>(p, layout, s);
+        case kQ5_K: return launch_l<Q5K>(p, layout, s);
         case kQ6_K: return launch_l<Q6K>(p, layout, s);
         case kQ8_0: return launch_l<Q80>(p, layout, s);
         default: return hipErrorInvalidValue;

@@ -60,16 +60,20 @@ __device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16)
 __device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
 __device__ __forceinline__ uint32_t u4(const uint4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
 
-// ------------------------------------------------------------------ Q4_K --
-struct MmaQ4K {
+// ------------------------------------------------------------ Q4_K, Q5_K --
+// Q5_K is Q4_K with a fifth code bit per weight: bit j of qh[l] for position l
+// of group j (exec:953-969), added to the operand bytes as 16.
+template <bool Q5>
+struct MmaQ4KT {
     static constexpr int kGroups = 8;  // 32-weight groups per unit
-    static constexpr int kUnitBytes = kQ4KUnit;
+    static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
     // The min term's token factor: dx * (sum of the 32 codes).
     __device__ static float stage_aux(float d, uint32_t s) { return d * (float)(s_lo(s) + s_hi(s)); }
     struct Frag {
         uint2 qs[4];  // bytes 32 g + 8 q .. +8 of the row's quants, g = 0..3
         uint4 h;      // d | dmin, scales[12]
+        uint2 qh;     // Q5_K: qh bytes 8 q .. +8
     };
     // unit: start of the 8-row TILED unit holding row i
     __device__ static Frag load(const uint8_t *unit, int i, int q) {
@@ -78,12 +82,18 @@ struct MmaQ4K {
 #pragma unroll
         for (int g = 0; g < 4; ++g) f.qs[g] = *(const uint2 *)(qs + 32 * g);
         f.h = *(const uint4 *)(unit + 16 * i);
+        if constexpr (Q5) f.qh = *(const uint2 *)(unit + kQ5KTQh + 32 * i + 8 * q);
         return f;
     }
     __device__ static long operand(const Frag &f, int j) {
         const uint2 w = f.qs[j >> 1];
         const int sh = 4 * (j & 1);
-        return as_long((w.x >> sh) & 0x0f0f0f0fu, (w.y >> sh) & 0x0f0f0f0fu);
+        uint32_t lo = (w.x >> sh) & 0x0f0f0f0fu, hi = (w.y >> sh) & 0x0f0f0f0fu;
+        if constexpr (Q5) {
+            lo |= ((f.qh.x >> j) & 0x01010101u) << 4;
+            hi |= ((f.qh.y >> j) & 0x01010101u) << 4;
+        }
+        return as_long(lo, hi);
     }
     // Main term: acc[t][e] += d sc_j * dx_j,e * S_j,e per group (VALU, the
     // group's integer sums from the MFMA).  Min term: cm[t] += sum_j aux_j,tok *
@@ -132,6 +142,9 @@ struct MmaQ4K {
         }
     }
 };
+
+using MmaQ4K = MmaQ4KT<false>;
+using MmaQ5K = MmaQ4KT<true>;
 
 // ------------------------------------------------------------------ Q6_K --
 struct MmaQ6K {
@@ -474,6 +487,7 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
 size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
     switch (type) {
         case kQ4_K: return mfma_lds<MmaQ4K, 16, 1>(upr);
+        case kQ5_K: return mfma_lds<MmaQ5K, 16, 1>(upr);
         case kQ6_K: return mfma_lds<MmaQ6K, 16, 1>(upr);
         case kQ8_0: return mfma_lds<MmaQ80, 16, 1>(upr);
         default: return 0;
@@ -483,6 +497,7 @@ size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
 hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
         case kQ4_K: return launch_mfma_cfg<MmaQ4K>(p, s);
+        case kQ5_K: return launch_mfma_cfg<MmaQ5K>(p, s);
         case kQ6_K: return launch_mfma_cfg<MmaQ6K>(p, s);
         case kQ8_0: return launch_mfma_cfg<MmaQ80>(p, s);
         default: return hipErrorInvalidValue;

@@ -129,11 +129,15 @@ struct Q4K {
         shi = dot4((int)((f.q.y >> 4) & kM4), a.hi.y, shi);
         shi = dot4((int)((f.q.z >> 4) & kM4), a.hi.z, shi);
         shi = dot4((int)((f.q.w >> 4) & kM4), a.hi.w, shi);
-        const uint32_t pair = scale_pair(f.h, L);
-        const int m = min_c(f.h, L);
+        return combine(f.h, a, L, slo, shi);
+    }
+    // The scale terms of the lane's two 16-value halves from their integer sums.
+    __device__ static float combine(const uint4 &h, const AFrag &a, const Lane &L, int slo, int shi) {
+        const uint32_t pair = scale_pair(h, L);
+        const int m = min_c(h, L);
         // |code sums| < 2^16 and scales < 2^6: the 24-bit products are exact.
         const float t = fmaf(a.dx.y, (float)__mul24((int)(pair >> 8), shi), a.dx.x * (float)__mul24((int)(pair & 0xffu), slo));
-        const float dw = f16_bits_to_f32(f.h.x), dm = f16_bits_to_f32(f.h.x >> 16);
+        const float dw = f16_bits_to_f32(h.x), dm = f16_bits_to_f32(h.x >> 16);
         return fmaf(dw, t, -dm * ((float)m * a.dsum));
     }
     __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
@@ -152,11 +156,87 @@ struct Q4K {
             flo += ubyte_f(lo, 0) * vl.x + ubyte_f(lo, 1) * vl.y + ubyte_f(lo, 2) * vl.z + ubyte_f(lo, 3) * vl.w;
             fhi += ubyte_f(hi, 0) * vh.x + ubyte_f(hi, 1) * vh.y + ubyte_f(hi, 2) * vh.z + ubyte_f(hi, 3) * vh.w;
         }
-        const uint32_t pair = scale_pair(f.h, L);
-        const int m = min_c(f.h, L);
+        return combine_f32(f.h, a, u, L, flo, fhi);
+    }
+    __device__ static float combine_f32(const uint4 &h, const ActLdsF32 &a, int u, const Lane &L, float flo,
+                                        float fhi) {
+        const uint32_t pair = scale_pair(h, L);
+        const int m = min_c(h, L);
         const float xsum = a.x16[16 * u + 2 * L.c] + a.x16[16 * u + 2 * L.c + 1];
-        const float dw = f16_bits_to_f32(f.h.x), dm = f16_bits_to_f32(f.h.x >> 16);
+        const float dw = f16_bits_to_f32(h.x), dm = f16_bits_to_f32(h.x >> 16);
         return dw * ((float)(pair & 0xffu) * flo + (float)(pair >> 8) * fhi) - dm * ((float)m * xsum);
+    }
+};
+
+// ------------------------------------------------------------------ Q5_K --
+// Q4_K plus a fifth bit per weight (exec:953-969): position l of 32-group j
+// adds 16 * bit j of qh[l].  Lane c reads the same 16 qs bytes as for Q4_K
+// and the 16 qh bytes of its half (qh[16 (c % 2) .. + 16)), whose bits 2g and
+// 2g + 1 (g = c / 2) belong to its low and high nibbles.  Everything else --
+// the activation fragment, the scales, the min term -- is Q4_K's.
+struct Q5K : Q4K {
+    static constexpr uint32_t kType = kQ5_K;
+    static constexpr int kUnitBytes = kQ5KUnit;
+    static constexpr int kBlockBytes = kQ5KBytes;
+
+    struct Frag {
+        uint4 q;   // 16 qs bytes
+        uint4 hb;  // 16 qh bytes
+        uint4 h;   // d | dmin << 16, scales[12]
+    };
+
+    __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
+        return {ld_u128(unit + 128 + 128 * i + 16 * c), ld_u128(unit + kQ5KTQh + 32 * i + 16 * (c & 1)),
+                ld_u128(unit + 16 * i)};
+    }
+    __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
+        const uint8_t *blk = row + (size_t)u * kQ5KBytes;
+        return {ld_u128(blk + kQ5KQs + 16 * c), ld_u128(blk + kQ5KQh + 16 * (c & 1)), ld_u128(blk)};
+    }
+
+    // 5-bit codes of one dword: the nibbles plus bit 2g (low) / 2g + 1 (high)
+    // of each qh byte, moved to bit 4.  Shifted right first: a left shift of the
+    // whole word would drop the top byte's bits 4..7 (groups 4..7).
+    __device__ static void codes(uint32_t q, uint32_t hb, const Lane &L, uint32_t &lo, uint32_t &hi) {
+        lo = (q & kM4) | (((hb >> (2 * L.g)) & 0x01010101u) << 4);
+        hi = ((q >> 4) & kM4) | (((hb >> (2 * L.g + 1)) & 0x01010101u) << 4);
+    }
+
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        const uint32_t hw[4] = {f.hb.x, f.hb.y, f.hb.z, f.hb.w};
+        const int alo[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w};
+        const int ahi[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo, hi;
+            codes(qw[k], hw[k], L, lo, hi);
+            slo = dot4((int)lo, alo[k], slo);
+            shi = dot4((int)hi, ahi[k], shi);
+        }
+        // |code sums| <= 16 * 31 * 127 < 2^16: the 24-bit scale products stay exact
+        return combine(f.h, a, L, slo, shi);
+    }
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        return dot(f, load_act(a, u, L), L);
+    }
+
+    __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
+        const float4 *xl = (const float4 *)(a.xf + 256 * u + L.off);
+        const float4 *xh = (const float4 *)(a.xf + 256 * u + L.off + 32);
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        const uint32_t hw[4] = {f.hb.x, f.hb.y, f.hb.z, f.hb.w};
+        float flo = 0.f, fhi = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo, hi;
+            codes(qw[k], hw[k], L, lo, hi);
+            const float4 vl = xl[k], vh = xh[k];
+            flo += ubyte_f(lo, 0) * vl.x + ubyte_f(lo, 1) * vl.y + ubyte_f(lo, 2) * vl.z + ubyte_f(lo, 3) * vl.w;
+            fhi += ubyte_f(hi, 0) * vh.x + ubyte_f(hi, 1) * vh.y + ubyte_f(hi, 2) * vh.z + ubyte_f(hi, 3) * vh.w;
+        }
+        return combine_f32(f.h, a, u, L, flo, fhi);
     }
 };
 

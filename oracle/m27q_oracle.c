@@ -19,6 +19,7 @@ size_t ora_type_size(int type) {
         case ORA_F16: return 2;
         case ORA_Q8_0: return 34;
         case ORA_Q4_K: return 144;
+        case ORA_Q5_K: return 176;
         case ORA_Q6_K: return 210;
         case ORA_Q8_K: return 292;
         default: return 0;
@@ -30,7 +31,7 @@ int ora_block_elems(int type) {
     switch (type) {
         case ORA_F32: case ORA_F16: return 1;
         case ORA_Q8_0: return 32;
-        case ORA_Q4_K: case ORA_Q6_K: case ORA_Q8_K: return 256;
+        case ORA_Q4_K: case ORA_Q5_K: case ORA_Q6_K: case ORA_Q8_K: return 256;
         default: return 0;
     }
 }
@@ -132,6 +133,31 @@ void ora_dequant_row_q4_K(const void *blocks, float *y, int64_t k) {
     }
 }
 
+/* exec:953-969 (q5k_val); ggml's dequantize_row_q5_K semantics.  As Q4_K, with a
+ * fifth bit: the value at position l of sub-block j (j = 2g + hi, l in [0,32))
+ * is the nibble of qs[32g+l] plus 16 * bit j of qh[l]. */
+void ora_dequant_row_q5_K(const void *blocks, float *y, int64_t k) {
+    const ora_block_q5_K *x = (const ora_block_q5_K *)blocks;
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = ora_fp16_to_fp32(x[i].d);
+        const float dmin = ora_fp16_to_fp32(x[i].dmin);
+        const uint8_t *q = x[i].qs;
+        for (int g = 0; g < 4; ++g) {
+            uint8_t sc, m;
+            ora_get_scale_min_k4(2 * g, x[i].scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            ora_get_scale_min_k4(2 * g + 1, x[i].scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l)
+                *y++ = d1 * (float)((q[l] & 0x0f) + (((x[i].qh[l] >> (2 * g)) & 1) << 4)) - m1;
+            for (int l = 0; l < 32; ++l)
+                *y++ = d2 * (float)((q[l] >> 4) + (((x[i].qh[l] >> (2 * g + 1)) & 1) << 4)) - m2;
+            q += 32;
+        }
+    }
+}
+
 /* exec:1026-1048 (q6k_val); debug/verify/verify_q6k_wqkv.py:5-34.
  * For half h, l in [0,32), r in [0,4): q_r = 6-bit value (low nibble of ql[64h+l] or
  * ql[64h+32+l], high nibble for r>=2; two bits 2r of qh[32h+l]) - 32;
@@ -181,6 +207,7 @@ int ora_dequant_rows(int type, const void *w, int rb, int rc, float *y) {
         float *yr = y + (size_t)r * k;
         switch (type) {
             case ORA_Q4_K: ora_dequant_row_q4_K(row, yr, k); break;
+            case ORA_Q5_K: ora_dequant_row_q5_K(row, yr, k); break;
             case ORA_Q6_K: ora_dequant_row_q6_K(row, yr, k); break;
             case ORA_Q8_0: ora_dequant_row_q8_0(row, yr, k); break;
             case ORA_F16: ora_fp16_to_fp32_n((const uint16_t *)row, yr, (size_t)k); break;
@@ -238,6 +265,55 @@ void ora_quantize_row_q4_K(const float *x, void *blocks, int64_t k) {
         for (int g = 0; g < 4; ++g)
             for (int l = 0; l < 32; ++l)
                 y[i].qs[32 * g + l] = (uint8_t)(L[64 * g + l] | (L[64 * g + 32 + l] << 4));
+    }
+}
+
+/* Q5_K generator: the Q4_K fit with 31 levels, the fifth bit into qh. */
+void ora_quantize_row_q5_K(const float *x, void *blocks, int64_t k) {
+    ora_block_q5_K *y = (ora_block_q5_K *)blocks;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        float scale[8], mn[8], maxs = 0.f, maxm = 0.f;
+        for (int j = 0; j < 8; ++j) {
+            float lo = 0.f, hi = 0.f;
+            for (int l = 0; l < 32; ++l) {
+                const float v = x[32 * j + l];
+                if (v < lo) lo = v;
+                if (v > hi) hi = v;
+            }
+            scale[j] = (hi - lo) / 31.f;
+            mn[j] = -lo;
+            if (scale[j] > maxs) maxs = scale[j];
+            if (mn[j] > maxm) maxm = mn[j];
+        }
+        const uint16_t dh = ora_fp32_to_fp16(maxs / 63.f), mh = ora_fp32_to_fp16(maxm / 63.f);
+        const float d = ora_fp16_to_fp32(dh), dmin = ora_fp16_to_fp32(mh);
+        uint8_t sc[8], m[8];
+        for (int j = 0; j < 8; ++j) {
+            sc[j] = (uint8_t)(d > 0.f ? clampi((int)lrintf(scale[j] / d), 0, 63) : 0);
+            m[j] = (uint8_t)(dmin > 0.f ? clampi((int)lrintf(mn[j] / dmin), 0, 63) : 0);
+        }
+        y[i].d = dh;
+        y[i].dmin = mh;
+        for (int j = 0; j < 4; ++j) {
+            y[i].scales[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            y[i].scales[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+            y[i].scales[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t L[256];
+        for (int j = 0; j < 8; ++j) {
+            const float ds = d * (float)sc[j], dm = dmin * (float)m[j];
+            for (int l = 0; l < 32; ++l) {
+                const float v = x[32 * j + l];
+                L[32 * j + l] = (uint8_t)(ds > 0.f ? clampi((int)lrintf((v + dm) / ds), 0, 31) : 0);
+            }
+        }
+        memset(y[i].qh, 0, 32);
+        for (int g = 0; g < 4; ++g)
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t a = L[64 * g + l], b = L[64 * g + 32 + l];
+                y[i].qs[32 * g + l] = (uint8_t)((a & 15) | ((b & 15) << 4));
+                y[i].qh[l] |= (uint8_t)(((a >> 4) << (2 * g)) | ((b >> 4) << (2 * g + 1)));
+            }
     }
 }
 
@@ -367,6 +443,28 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
                 nrm += fabs(t1) + fabs(t2);
             }
         }
+    } else if (type == ORA_Q5_K) {
+        /* as Q4_K with 5-bit codes (exec:421-495 semantics) */
+        const ora_block_q5_K *w = (const ora_block_q5_K *)wrow;
+        for (int b = 0; b < rb; ++b) {
+            const double dw = ora_fp16_to_fp32(w[b].d), dm = ora_fp16_to_fp32(w[b].dmin);
+            for (int j = 0; j < 8; ++j) {
+                uint8_t sc, m;
+                ora_get_scale_min_k4(j, w[b].scales, &sc, &m);
+                const int g = j / 2, hi = j & 1;
+                int sumi = 0;
+                for (int l = 0; l < 32; ++l) {
+                    const int nib = hi ? (w[b].qs[32 * g + l] >> 4) : (w[b].qs[32 * g + l] & 15);
+                    const int qw = nib + (((w[b].qh[l] >> j) & 1) << 4);
+                    sumi += qw * q[256 * b + 32 * j + l];
+                }
+                const int S = s16lo(s[8 * b + j]) + s16hi(s[8 * b + j]);
+                const double dx = d[8 * b + j];
+                const double t1 = dw * sc * dx * sumi, t2 = dm * m * dx * S;
+                acc += t1 - t2;
+                nrm += fabs(t1) + fabs(t2);
+            }
+        }
     } else if (type == ORA_Q6_K) {
         const ora_block_q6_K *w = (const ora_block_q6_K *)wrow;
         for (int b = 0; b < rb; ++b) {
@@ -408,7 +506,7 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
 int ora_gemv_act(int type, const void *w, int rb, int rc, const int8_t *q, const float *d,
                  const uint32_t *s, double *y, double *norm) {
     const size_t ts = ora_type_size(type);
-    if (!ts || (type != ORA_Q4_K && type != ORA_Q6_K && type != ORA_Q8_0)) return -1;
+    if (!ts || (type != ORA_Q4_K && type != ORA_Q5_K && type != ORA_Q6_K && type != ORA_Q8_0)) return -1;
     for (int r = 0; r < rc; ++r)
         y[r] = ora_dot_act(type, (const uint8_t *)w + (size_t)r * rb * ts, rb, q, d, s, norm ? norm + r : NULL);
     return 0;
@@ -487,6 +585,52 @@ float ora_ref_vec_dot_q4_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int 
                 const int v0i = (v0 >> (4 * i)) & 0x0f0f0f0f, v1i = (v1 >> (4 * i)) & 0x0f0f0f0f;
                 const int dot1 = dp4(v1i, u1, dp4(v0i, u0, 0));
                 const int dot2 = dp4(0x01010101, u1, dp4(0x01010101, u0, 0));
+                sumf_d += d8 * (float)(dot1 * sc[i]);
+                sumf_m += d8 * (float)(dot2 * m[i]);
+            }
+            total += ora_fp16_to_fp32(bq->d) * sumf_d - ora_fp16_to_fp32(bq->dmin) * sumf_m;
+        }
+    }
+    return total;
+}
+
+/* exec:421-495 (vec_dot_q5_K_q8_1 + _impl_vmmq): one thread's share iqs in
+ * {0,2,..,30} of one block, summed.  The fifth bit comes from qh[] shifted by
+ * the q8_1 block offset, per byte (vh >> i) << 4 & 0x10. */
+float ora_ref_vec_dot_q5_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb) {
+    const ora_block_q5_K *w = (const ora_block_q5_K *)wrow;
+    float total = 0.f;
+    for (int kbx = 0; kbx < rb; ++kbx) {
+        const ora_block_q5_K *bq = w + kbx;
+        const ora_block_q8_1 *b8 = xq + 8 * kbx;
+        for (int iqs = 0; iqs < 32; iqs += 2) {
+            const int bq8_offset = 2 * ((iqs / 2) / 4);
+            const uint8_t *ql = bq->qs + 16 * bq8_offset + 4 * ((iqs / 2) % 4);
+            const uint8_t *qh = bq->qh + 4 * ((iqs / 2) % 4);
+            const int vl0 = load_i32(ql), vl1 = load_i32(ql + 16);
+            const int vh0 = (int)((uint32_t)load_i32(qh) >> bq8_offset);
+            const int vh1 = (int)((uint32_t)load_i32(qh + 16) >> bq8_offset);
+            uint16_t sc16[6], aux[2];
+            memcpy(sc16, bq->scales, 12);
+            const int j = bq8_offset / 2;
+            if (j < 2) {
+                aux[0] = (uint16_t)(sc16[j + 0] & 0x3f3f);
+                aux[1] = (uint16_t)(sc16[j + 2] & 0x3f3f);
+            } else {
+                aux[0] = (uint16_t)(((sc16[j + 2] >> 0) & 0x0f0f) | ((sc16[j - 2] & 0xc0c0) >> 2));
+                aux[1] = (uint16_t)(((sc16[j + 2] >> 4) & 0x0f0f) | ((sc16[j - 0] & 0xc0c0) >> 2));
+            }
+            const uint8_t *sc = (const uint8_t *)aux, *m = sc + 2;
+            float sumf_d = 0.f, sumf_m = 0.f;
+            for (int i = 0; i < 2; ++i) {
+                const ora_block_q8_1 *b8i = b8 + bq8_offset + i;
+                const float d8 = ora_fp16_to_fp32(b8i->d);
+                const int u0 = load_i32(b8i->qs + 4 * ((iqs / 2) % 4));
+                const int u1 = load_i32(b8i->qs + 4 * ((iqs / 2) % 4) + 16);
+                const int vl0i = (vl0 >> (4 * i)) & 0x0f0f0f0f, vl1i = (vl1 >> (4 * i)) & 0x0f0f0f0f;
+                const int vh0i = ((vh0 >> i) << 4) & 0x10101010, vh1i = ((vh1 >> i) << 4) & 0x10101010;
+                const int dot1 = dp4(vl0i | vh0i, u0, dp4(vl1i | vh1i, u1, 0));
+                const int dot2 = dp4(0x01010101, u0, dp4(0x01010101, u1, 0));
                 sumf_d += d8 * (float)(dot1 * sc[i]);
                 sumf_m += d8 * (float)(dot2 * m[i]);
             }

@@ -21,6 +21,11 @@
  *                         dequantize_row_q4_K compiled from debug/official_dequant.c,
  *                         and the reference's second formulation (the dp4a vec-dot,
  *                         ora_ref_vec_dot_q4_K_q8_1) with one-hot activations.
+ *   ora_dequant_row_q5_K  the reference's dp4a vec-dot formulation
+ *                         (ora_ref_vec_dot_q5_K_q8_1, exec:421-495) with one-hot
+ *                         activations; with qh = 0 it equals ora_dequant_row_q4_K
+ *                         on the same d / dmin / scales / qs (pinned above), and
+ *                         setting qh bit j adds exactly 16 d sc_j to sub-block j.
  *   ora_dequant_row_q6_K  the reference's dp4a vec-dot formulation
  *                         (ora_ref_vec_dot_q6_K_q8_1, exec:586-628) with one-hot
  *                         activations, plus single-bit known answers.
@@ -49,10 +54,11 @@ extern "C" {
 #endif
 
 /* ggml type ids (include/mono27b_gguf.h:27-43 in the reference). */
-enum { ORA_F32 = 0, ORA_F16 = 1, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q6_K = 14, ORA_Q8_K = 15 };
+enum { ORA_F32 = 0, ORA_F16 = 1, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q5_K = 13, ORA_Q6_K = 14, ORA_Q8_K = 15 };
 
 /* GGUF block layouts (exec:18-23, :25-28, :38-42, :57-62). */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } ora_block_q4_K;
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } ora_block_q5_K; /* exec:30-36 */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } ora_block_q6_K;
 typedef struct { uint16_t d; int8_t qs[32]; } ora_block_q8_0;
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } ora_block_q8_K;
@@ -71,6 +77,7 @@ void ora_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
 
 /* Dequantization of k = n_blocks * block_elems weights. */
 void ora_dequant_row_q4_K(const void *blocks, float *y, int64_t k);
+void ora_dequant_row_q5_K(const void *blocks, float *y, int64_t k);
 void ora_dequant_row_q6_K(const void *blocks, float *y, int64_t k);
 void ora_dequant_row_q8_0(const void *blocks, float *y, int64_t k);
 /* rc rows of rb blocks each, GGUF row-major; F16/F32 rows of rb elements. */
@@ -78,6 +85,7 @@ int  ora_dequant_rows(int type, const void *w, int rb, int rc, float *y);
 
 /* Seeded block generators (own simple min/max quantizers). */
 void ora_quantize_row_q4_K(const float *x, void *blocks, int64_t k);
+void ora_quantize_row_q5_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k);
 
@@ -104,6 +112,7 @@ int ora_gemv_f64(int type, const void *w, int rb, int rc, const float *x, double
  * cross-check the dequant restatements (two independent codings of one format). */
 void  ora_quant_q8_1(const float *x, int64_t k, ora_block_q8_1 *y);
 float ora_ref_vec_dot_q4_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
+float ora_ref_vec_dot_q5_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 float ora_ref_vec_dot_q6_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 float ora_ref_vec_dot_q8_0_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 

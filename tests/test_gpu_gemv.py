@@ -17,6 +17,8 @@ SHAPES = {  # (type, rows, K)
     "q4k_small": ("Q4_K", 40, 512),
     "q4k_ffn": ("Q4_K", 17408, 5120),
     "q4k_o": ("Q4_K", 5120, 6144),
+    "q5k_gate": ("Q5_K", 6144, 5120),
+    "q5k_small": ("Q5_K", 24, 768),
     "q6k_down": ("Q6_K", 5120, 17408),
     "q6k_small": ("Q6_K", 24, 768),
     "q80_2048": ("Q8_0", 2048, 2048),
@@ -160,7 +162,7 @@ def test_multi_matches_single(m27q, ora, dev):
         assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K"])
 def test_ffn_swiglu(m27q, ora, dev, type_name):
     import torch
     t = getattr(m27q, type_name)
@@ -197,7 +199,7 @@ def check_swiglu(ora, t, gb, ub, rc, q, d, s, y):
     assert (err <= tol).all(), (np.flatnonzero(err > tol)[:5], err.max())
 
 
-@pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged"])
+@pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged", "q5k_gate", "q5k_small"])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_matvec_f32_vs_fp64(m27q, ora, dev, shape, layout):
     import torch
@@ -236,7 +238,7 @@ def test_matvec_dense(m27q, ora, dev, type_name):
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 5120, 6144), ("Q4_K", 17408, 5120),
-                                             ("Q8_0", 2048, 6144)])
+                                             ("Q8_0", 2048, 6144), ("Q5_K", 5120, 6144)])
 def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so at
     shapes where both input forms launch the same workgroup shape the product
@@ -259,7 +261,8 @@ def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
 
 
-@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 6144, 5120), ("Q8_0", 13, 160), ("Q4_K", 40, 512)])
+@pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 6144, 5120), ("Q8_0", 13, 160), ("Q4_K", 40, 512),
+                                             ("Q5_K", 6144, 5120)])
 def test_fp32_input_vs_oracle(m27q, ora, dev, type_name, rc, k):
     """Shapes where the fp32-input product launches its own workgroup shape:
     against the integer-dot oracle on the codes of the standalone quantizer."""

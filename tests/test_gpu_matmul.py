@@ -18,6 +18,8 @@ CASES = [  # type, rows, K, M, layout
     # 8-row tiles, each type
     ("Q6_K", 5120, 17408, 2, 1), ("Q6_K", 24, 768, 4, 1), ("Q4_K", 40, 512, 3, 1), ("Q8_0", 13, 160, 3, 1),
     ("Q8_0", 2048, 6144, 4, 1),
+    # Q5_K on each path: few-token GEMV, MFMA, GGUF VALU
+    ("Q5_K", 6144, 5120, 2, 1), ("Q5_K", 6144, 5120, 16, 1), ("Q5_K", 40, 512, 9, 1), ("Q5_K", 40, 512, 3, 0),
 ]
 
 

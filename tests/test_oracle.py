@@ -4,9 +4,11 @@
 - Q4_K dequant: the reference's known-answer block (official_dequant.c bytes ->
   the values the reference's GPU embed wrote), and dequantize_row_q4_K compiled
   from the reference's debug/official_dequant.c (oracle/_ref) on random blocks.
-- Q4_K / Q6_K / Q8_0 dequant: the reference's *other* formulation of each
-  format, its dp4a vec-dot (exec:250-310, :586-628, :535-580), driven with a
-  one-hot activation so that it returns one dequantized weight per position.
+- Q4_K / Q5_K / Q6_K / Q8_0 dequant: the reference's *other* formulation of
+  each format, its dp4a vec-dot (exec:250-310, :421-495, :586-628, :535-580),
+  driven with a one-hot activation so that it returns one dequantized weight
+  per position.
+- Q5_K dequant also reduces to the pinned Q4_K dequant when qh = 0.
 - int-dot oracle: numpy fp64 matmul of dequantized weights and activations.
 - activation quantizer: closed-form properties and constructed ties.
 - top-k: numpy lexsort.
@@ -27,7 +29,7 @@ def random_blocks(ora, type_, nblocks, rng=RNG):
     ts = ora.TYPE_SIZE[type_]
     b = rng.integers(0, 256, size=(nblocks, ts), dtype=np.uint8)
     f16 = lambda n: (rng.standard_normal(n) * 0.05).astype(np.float16).view(np.uint16)
-    if type_ == ora.Q4_K:
+    if type_ in (ora.Q4_K, ora.Q5_K):
         b[:, 0:2] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
         b[:, 2:4] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
     elif type_ == ora.Q6_K:
@@ -37,7 +39,7 @@ def random_blocks(ora, type_, nblocks, rng=RNG):
     # a few subnormal / zero scales
     sub = np.array([0x0001, 0x03ff, 0x8001, 0x0000, 0x8000], np.uint16).view(np.uint8).reshape(5, 2)
     for i in range(min(5, nblocks)):
-        off = {ora.Q4_K: 0, ora.Q6_K: 208, ora.Q8_0: 0}[type_]
+        off = {ora.Q4_K: 0, ora.Q5_K: 0, ora.Q6_K: 208, ora.Q8_0: 0}[type_]
         b[i, off:off + 2] = sub[i]
     return b
 
@@ -82,7 +84,7 @@ def test_q4k_matches_reference_c_build(ora):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
 def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
     """x = 127 e_j quantizes to d = 1, code 127 at j: the reference's dp4a dot then
     returns 127 * W[j] (rounded once or twice), which pins every position's
@@ -91,6 +93,20 @@ def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
     be = ora.BLOCK_ELEMS[t]
     rb = 2 if t != ora.Q8_0 else 8
     k = rb * be
+
+    def f16(b, off):
+        return abs(float(np.frombuffer(b[off:off + 2].tobytes(), np.float16)[0]))
+
+    def term_bound(b):
+        # largest |term| the fp32 combine of the reference's formulation can round:
+        # 127 x (max scale) x (max code) x (block scale), per block
+        if t in (ora.Q4_K, ora.Q5_K):
+            qmax = 15 if t == ora.Q4_K else 31
+            return 127.0 * 63 * (qmax * f16(b, 0) + f16(b, 2))
+        if t == ora.Q6_K:
+            return 127.0 * 128 * 32 * f16(b, 208)
+        return 127.0 * 128 * f16(b, 0)
+
     for trial in range(3):
         blocks = random_blocks(ora, t, rb, np.random.default_rng(trial))
         deq = ora.dequant(t, blocks, rb, 1)[0].astype(np.float64)
@@ -99,7 +115,8 @@ def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
             x[j] = 127.0
             xq = ora.quant_q8_1(x)
             v = ora.ref_vec_dot_q8_1(t, blocks.reshape(-1), xq, rb)
-            assert abs(v - 127.0 * deq[j]) <= 4e-7 * abs(127.0 * deq[j]) + 1e-30, (type_name, trial, j)
+            tol = max(4e-7 * abs(127.0 * deq[j]), 2.0 ** -22 * term_bound(blocks[j // be])) + 1e-30
+            assert abs(v - 127.0 * deq[j]) <= tol, (type_name, trial, j)
 
 
 def test_q6k_single_bit_layout(ora):
@@ -118,7 +135,54 @@ def test_q6k_single_bit_layout(ora):
     assert np.array_equal(y, want)
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K", "Q8_0"])
+def test_q5k_without_high_bits_is_q4k(ora):
+    """A Q5_K block with qh = 0 holds the same values as the Q4_K block with the
+    same d, dmin, scales and qs (Q4_K is pinned to the reference's C above)."""
+    q4 = random_blocks(ora, ora.Q4_K, 64)
+    q5 = np.zeros((64, 176), np.uint8)
+    q5[:, :16] = q4[:, :16]      # d, dmin, scales
+    q5[:, 48:176] = q4[:, 16:144]  # qs after qh[32]
+    a = ora.dequant(ora.Q4_K, q4, 64, 1)[0]
+    b = ora.dequant(ora.Q5_K, q5, 64, 1)[0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_q5k_high_bit_positions(ora):
+    """Bit j of qh[l] adds 16 to the code of position l of 32-group j, and only
+    there (the index map of exec:955-969)."""
+    rng = np.random.default_rng(3)
+    base = random_blocks(ora, ora.Q5_K, 1, rng)[0]
+    base[5:] = base[5:]  # keep random scales
+    base[16:48] = 0       # qh = 0
+    y0 = ora.dequant(ora.Q5_K, base, 1, 1)[0]
+    q4 = np.concatenate([base[:16], base[48:]])
+    for j in range(8):
+        for l in (0, 7, 31):
+            blk = base.copy()
+            blk[16 + l] |= np.uint8(1 << j)
+            y = ora.dequant(ora.Q5_K, blk, 1, 1)[0]
+            changed = np.flatnonzero(y.view(np.uint32) != y0.view(np.uint32))
+            pos = 32 * j + l
+            assert set(changed) <= {pos}
+            # the changed value: the Q4_K value of a block whose nibble is 16 larger
+            # cannot be written in Q4_K, so compare with d*sc*(q+16) - dmin*m
+            d = np.float32(np.frombuffer(q4[0:2].tobytes(), np.float16)[0])
+            dm = np.float32(np.frombuffer(q4[2:4].tobytes(), np.float16)[0])
+            sc, m = scale_min(q4[4:16], j)
+            nib = (q4[16 + 32 * (j // 2) + l] >> (4 * (j & 1))) & 15
+            want = np.float32(d * np.float32(sc)) * np.float32(nib + 16) - np.float32(dm * np.float32(m))
+            assert y[pos].view(np.uint32) == np.float32(want).view(np.uint32) or (np.isnan(y[pos]) and np.isnan(want))
+
+
+def scale_min(q, j):
+    """get_scale_min_k4 from the reference's byte description (exec:690-693)."""
+    q = [int(v) for v in q]
+    if j < 4:
+        return q[j] & 63, q[j + 4] & 63
+    return (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
 def test_int_dot_oracle_vs_numpy_bruteforce(ora, type_name):
     t = getattr(ora, type_name)
     be = ora.BLOCK_ELEMS[t]
