@@ -53,7 +53,8 @@ enum {
     M27Q_TYPE_Q8_0 = 8,
     M27Q_TYPE_Q4_K = 12,
     M27Q_TYPE_Q5_K = 13,
-    M27Q_TYPE_Q6_K = 14
+    M27Q_TYPE_Q6_K = 14,
+    M27Q_TYPE_IQ4_XS = 23
 };
 
 /* Weight layouts in device memory.
@@ -92,7 +93,7 @@ M27Q_API size_t m27q_weight_bytes(uint32_t ggml_type, uint32_t row_blocks, uint3
 
 /* GGUF rows -> TILED (host memory to host memory).  Replaces the verbatim
  * copy of lw() (exec:1695-1716) with pack-time re-tiling; the caller uploads
- * the result.  Supported types: Q4_K, Q5_K, Q6_K, Q8_0. */
+ * the result.  Supported types: Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS. */
 M27Q_API m27q_status m27q_repack(uint32_t ggml_type, uint32_t row_blocks, uint32_t row_count,
                                  const void *gguf_rows, void *tiled);
 /* TILED -> GGUF rows (the exact inverse of m27q_repack). */
@@ -128,8 +129,9 @@ M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int
 
 /* ------------------------------------------------------------------------
  * M = 1 matrix-vector products (integer dot: int8 activation codes x weight
- * codes, fp32 combine).  Q4_K, Q5_K, Q6_K, Q8_0 weights in either layout
- * (Q5_K: the vec_dot_q5_K_q8_1 / k_q5k_mv_q8 path of exec:421-531).
+ * codes, fp32 combine).  Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS weights in either
+ * layout (Q5_K: the vec_dot_q5_K_q8_1 / k_q5k_mv_q8 path of exec:421-531;
+ * IQ4_XS: vec_dot_iq4_xs_q8_1 / k_iq4xs_mv_q8_dp4a, exec:647-686).
  *
  * The activation is given either as fp32 values x[K] (16-byte aligned),
  * quantized inside the product with exactly the rule of m27q_quant_act (the
@@ -174,10 +176,10 @@ M27Q_API m27q_status m27q_ffn_swiglu_q8(const m27q_weight *gate, const m27q_weig
                                         void *yq, hipStream_t stream);
 
 /* fp32-activation product y = W x (+ residual): exact dequantization and fp32
- * accumulation.  Q4_K, Q5_K, Q6_K, Q8_0, F16, F32.  Replaces l_mv_fallback
- * (exec:2127-2137) with k_q4k_mv / k_q5k_mv / k_q6k_mt / k_q80_mv / k_f16_mv /
- * k_f32_mv (exec:920-951, :953-985, :1053-1072, :1076-1096, :899-916,
- * :1100-1114). */
+ * accumulation.  Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS, F16, F32.  Replaces
+ * l_mv_fallback (exec:2127-2137) with k_q4k_mv / k_q5k_mv / k_q6k_mt /
+ * k_q80_mv / k_iq4xs_mv / k_f16_mv / k_f32_mv (exec:920-951, :953-985,
+ * :1053-1072, :1076-1096, :992-1020, :899-916, :1100-1114). */
 M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float *y, const float *residual,
                                      hipStream_t stream);
 

@@ -48,7 +48,7 @@ m27q_status check_weight(const m27q_weight *w, bool quant_only) {
         if (!is_quant(t)) return M27Q_ERR_LAYOUT;
         if (!aligned(w->ptr, 16)) return M27Q_ERR_LAYOUT;
     } else if (w->layout == M27Q_LAYOUT_GGUF) {
-        const size_t need = (t == kQ6_K || t == kQ8_0) ? 2 : 16;
+        const size_t need = (t == kQ6_K || t == kQ8_0) ? 2 : (t == kIQ4_XS ? 8 : 16);
         if (!aligned(w->ptr, need)) return M27Q_ERR_LAYOUT;
         if (t == kF16 && (w->row_blocks % 8)) return M27Q_ERR_SHAPE;
         if (t == kF32 && (w->row_blocks % 4)) return M27Q_ERR_SHAPE;

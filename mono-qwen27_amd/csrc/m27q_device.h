@@ -123,4 +123,17 @@ __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uin
     return make_uint2(w0, w1);
 }
 
+// IQ4_NL / IQ4_XS table (exec:51-55) as bytes: entries 0..3, 4..7, 8..11, 12..15.
+constexpr uint32_t kIq4T0 = 0xBFAD9881u, kIq4T1 = 0xF6EADDCFu, kIq4T2 = 0x26190D01u, kIq4T3 = 0x71594535u;
+
+// Four 4-bit indices (one per byte, values 0..15) -> four int8 table values.
+// v_perm_b32 picks bytes of {S0, S1} by selector (0..3: S1, 4..7: S0): one
+// lookup in entries 0..7, one in 8..15, then a third picks per byte by bit 3.
+__device__ __forceinline__ uint32_t iq4_lut(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4T1, kIq4T0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4T3, kIq4T2, sel);
+    return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((n & 0x08080808u) >> 1));
+}
+
 }  // namespace m27q

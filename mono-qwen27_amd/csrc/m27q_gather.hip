@@ -133,6 +133,36 @@ __device__ __forceinline__ float4 cvt_q6k(const Raw &w, int l) {
     return make_float4(o[0], o[1], o[2], o[3]);
 }
 
+// IQ4_XS: lane l covers positions t .. t + 3 (t = 4 (l % 8)) of 32-group l / 8:
+// the low (t < 16) or high nibbles of qs bytes 16 g + t % 16 .. + 4.
+__device__ __forceinline__ Raw load_iq4xs(const GatherParams &p, int r, int b, int l) {
+    const int g = l >> 3, t = 4 * (l & 7);
+    Raw w;
+    const uint8_t *hdr, *qs;
+    if (p.layout == M27Q_LAYOUT_TILED) {
+        const uint8_t *unit = p.W + ((size_t)(r / kTileRows) * p.upr + b) * kIQ4XSUnit;
+        const int i = r % kTileRows;
+        qs = unit + 128 * i;
+        hdr = unit + kIQ4XSTHdr + 8 * i;
+    } else {
+        hdr = p.W + ((size_t)r * p.rb + b) * kIQ4XSBytes;
+        qs = hdr + kIQ4XSQs;
+    }
+    const uint2 hd = *(const uint2 *)hdr;
+    w.a.x = hd.x;
+    w.a.y = hd.y;
+    w.b = *(const uint32_t *)(qs + 16 * g + (t & 15));
+    return w;
+}
+__device__ __forceinline__ float4 cvt_iq4xs(const Raw &w, int l) {
+    const int g = l >> 3, t = 4 * (l & 7);
+    const int ls = (int)(((w.a.y >> (8 * (g >> 1) + 4 * (g & 1))) & 15u) | (((w.a.x >> (16 + 2 * g)) & 3u) << 4));
+    const float dl = f16_bits_to_f32(w.a.x) * (float)(ls - 32);
+    const uint32_t v = iq4_lut((w.b >> (t < 16 ? 0 : 4)) & 0x0f0f0f0fu);
+    return make_float4(dl * (float)(int8_t)v, dl * (float)(int8_t)(v >> 8), dl * (float)(int8_t)(v >> 16),
+                       dl * (float)(int8_t)(v >> 24));
+}
+
 // Q8_0: the lane's 4 values start at position k4 of block b.
 __device__ __forceinline__ Raw load_q80(const GatherParams &p, int r, int b, int k4) {
     Raw w;
@@ -186,6 +216,7 @@ __global__ __launch_bounds__(256) void k_gather(GatherParams p) {
         const int pos = min(ch * 256 + 4 * lane, K - 4);
         if constexpr (TYPE == kQ4_K) w[j] = load_q4k(p, r, ch, lane);
         else if constexpr (TYPE == kQ5_K) w[j] = load_q5k(p, r, ch, lane);
+        else if constexpr (TYPE == kIQ4_XS) w[j] = load_iq4xs(p, r, ch, lane);
         else if constexpr (TYPE == kQ6_K) w[j] = load_q6k(p, r, ch, lane);
         else if constexpr (TYPE == kQ8_0) w[j] = load_q80(p, r, pos / 32, pos % 32);  // K % 32 == 0
         else if constexpr (TYPE == kF16) {
@@ -203,6 +234,7 @@ __global__ __launch_bounds__(256) void k_gather(GatherParams p) {
         float4 v;
         if constexpr (TYPE == kQ4_K) v = cvt_q4k(w[j], lane);
         else if constexpr (TYPE == kQ5_K) v = cvt_q5k(w[j], lane);
+        else if constexpr (TYPE == kIQ4_XS) v = cvt_iq4xs(w[j], lane);
         else if constexpr (TYPE == kQ6_K) v = cvt_q6k(w[j], lane);
         else if constexpr (TYPE == kQ8_0) v = cvt_q80(w[j]);
         else if constexpr (TYPE == kF16)
@@ -221,6 +253,7 @@ hipError_t launch_gather(const GatherParams &p, hipStream_t s) {
     switch (p.type) {
         case kQ4_K: hipLaunchKernelGGL(k_gather<kQ4_K>, grid, block, 0, s, p); break;
         case kQ5_K: hipLaunchKernelGGL(k_gather<kQ5_K>, grid, block, 0, s, p); break;
+        case kIQ4_XS: hipLaunchKernelGGL(k_gather<kIQ4_XS>, grid, block, 0, s, p); break;
         case kQ6_K: hipLaunchKernelGGL(k_gather<kQ6_K>, grid, block, 0, s, p); break;
         case kQ8_0: hipLaunchKernelGGL(k_gather<kQ8_0>, grid, block, 0, s, p); break;
         case kF16: hipLaunchKernelGGL(k_gather<kF16>, grid, block, 0, s, p); break;

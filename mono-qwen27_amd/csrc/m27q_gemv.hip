@@ -27,11 +27,12 @@
 //
 // Replaces k_q4k_mv_q8_dp4a / k_q6k_mv_q8_dp4a / k_q80_mv_q8_dp4a
 // (exec:320-364, :631-645, :535-580), k_q5k_mv_q8 (exec:497-531),
+// k_iq4xs_mv_q8_dp4a (exec:674-686),
 // k_q4k_q4k_swiglu_dp4a (exec:369-417),
 // k_quant_q8_1 in front of them (exec:84-107, launched by l_quant_q8_n
 // :2022-2030) and the fp32 fallbacks k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv
-// / k_f32_mv / k_q5k_mv (exec:920-951, :1053-1072, :1076-1096, :899-916,
-// :1100-1114, :953-985).
+// / k_f32_mv / k_q5k_mv / k_iq4xs_mv (exec:920-951, :1053-1072, :1076-1096,
+// :899-916, :1100-1114, :953-985, :992-1020).
 #include "m27q_gemv_cfg.h"
 #include "m27q_internal.h"
 #include "m27q_types.h"
@@ -428,6 +429,7 @@ size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg) {
         case kQ5_K: return lds_for<Q5K>(upr, swiglu, cfg);
         case kQ6_K: return lds_for<Q6K>(upr, swiglu, cfg);
         case kQ8_0: return lds_for<Q80>(upr, swiglu, cfg);
+        case kIQ4_XS: return lds_for<IQ4XS>(upr, swiglu, cfg);
         default: return 0;
     }
 }
@@ -448,6 +450,7 @@ hipError_t launch_gemv_q8(uint32_t type, int layout, bool swiglu, int cfg, const
         case kQ5_K: return launch_q8_x<Q5K>(p, layout, swiglu, cfg, s);
         case kQ6_K: return launch_q8_x<Q6K>(p, layout, swiglu, cfg, s);
         case kQ8_0: return launch_q8_x<Q80>(p, layout, swiglu, cfg, s);
+        case kIQ4_XS: return launch_q8_x<IQ4XS>(p, layout, swiglu, cfg, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -477,6 +480,7 @@ hipError_t launch_gemv_f32(uint32_t type, int layout, const GemvParams &p, int g
         case kQ5_K: return launch_f32_l<Q5K>(p, layout, grid, s);
         case kQ6_K: return launch_f32_l<Q6K>(p, layout, grid, s);
         case kQ8_0: return launch_f32_l<Q80>(p, layout, grid, s);
+        case kIQ4_XS: return launch_f32_l<IQ4XS>(p, layout, grid, s);
         case kF16:
             hipLaunchKernelGGL((k_gemv_dense<true>), dim3(grid), dim3(256), 0, s, p);
             return hipGetLastError();

@@ -216,6 +216,7 @@ size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M) {
         case kQ5_K: return one(Q5K{});
         case kQ6_K: return one(Q6K{});
         case kQ8_0: return one(Q80{});
+        case kIQ4_XS: return one(IQ4XS{});
         default: return 0;
     }
 }
@@ -235,6 +236,7 @@ hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream
         case kQ5_K: return launch_mt_m<Q5K>(p, s);
         case kQ6_K: return launch_mt_m<Q6K>(p, s);
         case kQ8_0: return launch_mt_m<Q80>(p, s);
+        case kIQ4_XS: return launch_mt_m<IQ4XS>(p, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -51,6 +51,17 @@ void move_q6k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
     }
 }
 
+void move_iq4xs(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
+    uint8_t *qs = unit + 128 * i, *hdr = unit + kIQ4XSTHdr + 8 * i;
+    if (to_tiled) {
+        std::memcpy(hdr, blk, kIQ4XSQs);
+        std::memcpy(qs, blk + kIQ4XSQs, 128);
+    } else {
+        std::memcpy(blk, hdr, kIQ4XSQs);
+        std::memcpy(blk + kIQ4XSQs, qs, 128);
+    }
+}
+
 void move_q80(uint8_t *unit, int i, int k, uint8_t *blk, bool to_tiled) {
     uint8_t *qs = unit + 128 * i + 32 * k, *d = unit + kQ80TD + 8 * i + 2 * k;
     if (to_tiled) {
@@ -85,6 +96,7 @@ m27q_status convert(uint32_t type, uint32_t rb, uint32_t rc, const void *src, vo
                 uint8_t *unit = tiled + ((size_t)t * upr + b) * ub;
                 if (type == kQ4_K) move_q4k(unit, i, blk, to_tiled);
                 else if (type == kQ5_K) move_q5k(unit, i, blk, to_tiled);
+                else if (type == kIQ4_XS) move_iq4xs(unit, i, blk, to_tiled);
                 else move_q6k(unit, i, blk, to_tiled);
             }
         }

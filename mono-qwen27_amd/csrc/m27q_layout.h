@@ -12,17 +12,19 @@
 namespace m27q {
 
 // ggml type ids (include/mono27b_gguf.h:27-43).
-constexpr uint32_t kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14;
+constexpr uint32_t kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ4_XS = 23;
 
 // GGUF block sizes in bytes / weights (src/mono27b_gguf.cpp:167-195).
 constexpr int kQ4KBytes = 144;   // f16 d, f16 dmin, u8 scales[12], u8 qs[128]
 constexpr int kQ5KBytes = 176;   // f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
 constexpr int kQ6KBytes = 210;   // u8 ql[128], u8 qh[64], i8 scales[16], f16 d
 constexpr int kQ80Bytes = 34;    // f16 d, i8 qs[32]
+constexpr int kIQ4XSBytes = 136; // f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128] (exec:44-49)
 
 // Byte offsets inside one GGUF block.
 constexpr int kQ4KHdr = 16;      // d, dmin, scales: bytes [0, 16)
 constexpr int kQ5KQh = 16, kQ5KQs = 48;
+constexpr int kIQ4XSQs = 8;       // d, scales_h, scales_l: bytes [0, 8)
 constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 
 // ---------------------------------------------------------------- TILED --
@@ -43,6 +45,9 @@ constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 //        [1024, 1536)  8 x 64 B qh                             row i at 1024 + 64 i
 //        [1536, 1664)  8 x 16 B scales                         row i at 1536 + 16 i
 //        [1664, 1680)  8 x 2 B d                               row i at 1664 + 2 i
+//  IQ4_XS unit = one block column                         1088 B
+//        [0, 1024)     8 x 128 B qs                            row i at 128 i
+//        [1024, 1088)  8 x 8 B headers (d, scales_h, scales_l) row i at 1024 + 8 i
 //  Q8_0  unit = four block columns (128 weights)          1088 B
 //        [0, 1024)     8 rows x 4 blocks x 32 B qs             (i, k) at 128 i + 32 k
 //        [1024, 1088)  8 rows x 4 blocks x 2 B d               (i, k) at 1024 + 8 i + 2 k
@@ -58,13 +63,16 @@ constexpr int kQ4KUnit = kTileRows * kQ4KBytes;      // 1152
 constexpr int kQ5KUnit = kTileRows * kQ5KBytes;      // 1408
 constexpr int kQ5KTQh = 1152;
 constexpr int kQ6KUnit = kTileRows * kQ6KBytes;      // 1680
+constexpr int kIQ4XSUnit = kTileRows * kIQ4XSBytes;  // 1088
+constexpr int kIQ4XSTHdr = 1024;
 constexpr int kQ80UnitBlocks = 4;
 constexpr int kQ80Unit = kTileRows * kQ80UnitBlocks * kQ80Bytes;  // 1088
 
 constexpr int kQ6KTQl = 0, kQ6KTQh = 1024, kQ6KTSc = 1536, kQ6KTD = 1664;
 constexpr int kQ80TD = 1024;
 
-static_assert(kQ4KUnit % 16 == 0 && kQ5KUnit % 16 == 0 && kQ6KUnit % 16 == 0 && kQ80Unit % 16 == 0,
+static_assert(kQ4KUnit % 16 == 0 && kQ5KUnit % 16 == 0 && kQ6KUnit % 16 == 0 && kQ80Unit % 16 == 0 &&
+                  kIQ4XSUnit % 16 == 0,
               "every tiled unit keeps 16-byte alignment");
 
 inline int block_bytes(uint32_t type) {
@@ -73,6 +81,7 @@ inline int block_bytes(uint32_t type) {
         case kQ5_K: return kQ5KBytes;
         case kQ6_K: return kQ6KBytes;
         case kQ8_0: return kQ80Bytes;
+        case kIQ4_XS: return kIQ4XSBytes;
         case kF16: return 2;
         case kF32: return 4;
         default: return 0;
@@ -81,14 +90,16 @@ inline int block_bytes(uint32_t type) {
 
 inline int block_elems(uint32_t type) {
     switch (type) {
-        case kQ4_K: case kQ5_K: case kQ6_K: return 256;
+        case kQ4_K: case kQ5_K: case kQ6_K: case kIQ4_XS: return 256;
         case kQ8_0: return 32;
         case kF16: case kF32: return 1;
         default: return 0;
     }
 }
 
-inline bool is_quant(uint32_t type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0; }
+inline bool is_quant(uint32_t type) {
+    return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kIQ4_XS;
+}
 
 inline int tiles_of(uint32_t rows) { return (int)((rows + kTileRows - 1) / kTileRows); }
 
@@ -102,6 +113,7 @@ inline int unit_bytes(uint32_t type) {
         case kQ5_K: return kQ5KUnit;
         case kQ6_K: return kQ6KUnit;
         case kQ8_0: return kQ80Unit;
+        case kIQ4_XS: return kIQ4XSUnit;
         default: return 0;
     }
 }

@@ -119,6 +119,7 @@ hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hi
         case kQ5_K: return launch_l<Q5K>(p, layout, s);
         case kQ6_K: return launch_l<Q6K>(p, layout, s);
         case kQ8_0: return launch_l<Q80>(p, layout, s);
+        case kIQ4_XS: return launch_l<IQ4XS>(p, layout, s);
         default: return hipErrorInvalidValue;
     }
 }

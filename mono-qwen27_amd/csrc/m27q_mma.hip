@@ -277,6 +277,48 @@ struct MmaQ80 {
     }
 };
 
+// ---------------------------------------------------------------- IQ4_XS --
+// Group j of the block: lane quarter q holds positions 8 q .. 8 q + 7, the low
+// nibbles of qs bytes 16 j + 8 q (q < 2) or the high nibbles of 16 j + 8 (q - 2)
+// (q >= 2), through the 16-entry table; scale d (ls_j - 32) per group.
+struct MmaIQ4XS {
+    static constexpr int kGroups = 8;
+    static constexpr int kUnitBytes = kIQ4XSUnit;
+    static constexpr bool kAux = false;
+    __device__ static float stage_aux(float, uint32_t) { return 0.f; }
+    struct Frag {
+        uint2 qs[8];  // 8 qs bytes of each group
+        uint2 hd;     // d | scales_h << 16, scales_l[4]
+    };
+    __device__ static Frag load(const uint8_t *unit, int i, int q) {
+        Frag f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f.qs[j] = *(const uint2 *)(unit + 128 * i + 16 * j + 8 * (q & 1));
+        f.hd = *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i);
+        return f;
+    }
+    template <int RT>
+    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
+                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
+        const int nsh = q < 2 ? 0 : 4;
+#pragma unroll
+        for (int j = 0; j < kGroups; ++j) {
+            const float4 dx = sl.dx(g0 + j, q);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const uint2 w = f[t].qs[j];
+                const long b = as_long(iq4_lut((w.x >> nsh) & 0x0f0f0f0fu), iq4_lut((w.y >> nsh) & 0x0f0f0f0fu));
+                const v4i c = mfma32(a[j], b, v4i{0, 0, 0, 0});
+                const int ls = (int)(((f[t].hd.y >> (8 * (j >> 1) + 4 * (j & 1))) & 15u) |
+                                     (((f[t].hd.x >> (16 + 2 * j)) & 3u) << 4)) - 32;
+                const float dl = f16_bits_to_f32(f[t].hd.x) * (float)ls;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(dl * f4(dx, e), (float)c[e], acc[t][e]);
+            }
+        }
+    }
+};
+
 // One unit (a K range of kGroups x 32) of activation operands.
 template <class T>
 struct ActUnit {
@@ -490,6 +532,7 @@ size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
         case kQ5_K: return mfma_lds<MmaQ5K, 16, 1>(upr);
         case kQ6_K: return mfma_lds<MmaQ6K, 16, 1>(upr);
         case kQ8_0: return mfma_lds<MmaQ80, 16, 1>(upr);
+        case kIQ4_XS: return mfma_lds<MmaIQ4XS, 16, 1>(upr);
         default: return 0;
     }
 }
@@ -500,6 +543,7 @@ hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStre
         case kQ5_K: return launch_mfma_cfg<MmaQ5K>(p, s);
         case kQ6_K: return launch_mfma_cfg<MmaQ6K>(p, s);
         case kQ8_0: return launch_mfma_cfg<MmaQ80>(p, s);
+        case kIQ4_XS: return launch_mfma_cfg<MmaIQ4XS>(p, s);
         default: return hipErrorInvalidValue;
     }
 }

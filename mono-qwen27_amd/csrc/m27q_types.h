@@ -376,6 +376,85 @@ struct Q6K {
     }
 };
 
+// ---------------------------------------------------------------- IQ4_XS --
+// Lane c holds the 16 qs bytes of 32-group c: low nibbles are its positions
+// 0..15, high nibbles 16..31 (exec:992-1011).  Codes go through the 16-entry
+// table to int8 and into dot4; per group d (ls_c - 32) dx_c sum(kv[q] q8)
+// (vec_dot_iq4_xs_q8_1, exec:647-671).  GGUF blocks are 136 B: 8-byte loads.
+struct IQ4XS {
+    static constexpr uint32_t kType = kIQ4_XS;
+    static constexpr int kUnitElems = 256;
+    static constexpr int kUnitBytes = kIQ4XSUnit;
+    static constexpr int kBlockBytes = kIQ4XSBytes;
+
+    struct Frag {
+        uint4 q;   // 16 qs bytes of group c
+        uint2 hd;  // d | scales_h << 16, scales_l[4]
+    };
+    struct Lane {
+        int c, lsh, hsh;
+        __device__ explicit Lane(int c_) : c(c_), lsh(8 * (c_ >> 1) + 4 * (c_ & 1)), hsh(16 + 2 * c_) {}
+    };
+    struct AFrag {
+        int4 lo, hi;
+        float dx;
+    };
+
+    __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
+        return {ld_u128(unit + 128 * i + 16 * c), *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i)};
+    }
+    __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
+        const uint8_t *blk = row + (size_t)u * kIQ4XSBytes;
+        const uint2 a = *(const uint2 *)(blk + kIQ4XSQs + 16 * c), b = *(const uint2 *)(blk + kIQ4XSQs + 16 * c + 8);
+        return {make_uint4(a.x, a.y, b.x, b.y), *(const uint2 *)blk};
+    }
+    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }
+
+    __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
+        AFrag r;
+        r.lo = *(const int4 *)(a.xc + 256 * u + 32 * L.c);
+        r.hi = *(const int4 *)(a.xc + 256 * u + 32 * L.c + 16);
+        r.dx = a.xd[8 * u + L.c];
+        return r;
+    }
+    __device__ static int ls_minus_32(const uint2 &hd, const Lane &L) {
+        return (int)(((hd.y >> L.lsh) & 15u) | (((hd.x >> L.hsh) & 3u) << 4)) - 32;
+    }
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        const int alo[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w};
+        const int ahi[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s = dot4((int)iq4_lut(qw[k] & kM4), alo[k], s);
+            s = dot4((int)iq4_lut((qw[k] >> 4) & kM4), ahi[k], s);
+        }
+        // |s| <= 32 * 127 * 127 and |ls - 32| <= 32: the product is exact in 24 bits
+        return f16_bits_to_f32(f.hd.x) * a.dx * (float)__mul24(s, ls_minus_32(f.hd, L));
+    }
+    __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
+        return dot(f, load_act(a, u, L), L);
+    }
+
+    __device__ static float dot_f32(const Frag &f, const ActLdsF32 &a, int u, const Lane &L) {
+        const float4 *xl = (const float4 *)(a.xf + 256 * u + 32 * L.c);
+        const float4 *xh = (const float4 *)(a.xf + 256 * u + 32 * L.c + 16);
+        const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t vl = iq4_lut(qw[k] & kM4), vh = iq4_lut((qw[k] >> 4) & kM4);
+            const float4 x0 = xl[k], x1 = xh[k];
+            acc += (float)(int8_t)vl * x0.x + (float)(int8_t)(vl >> 8) * x0.y + (float)(int8_t)(vl >> 16) * x0.z +
+                   (float)(int8_t)(vl >> 24) * x0.w;
+            acc += (float)(int8_t)vh * x1.x + (float)(int8_t)(vh >> 8) * x1.y + (float)(int8_t)(vh >> 16) * x1.z +
+                   (float)(int8_t)(vh >> 24) * x1.w;
+        }
+        return f16_bits_to_f32(f.hd.x) * (float)ls_minus_32(f.hd, L) * acc;
+    }
+};
+
 // ------------------------------------------------------------------ Q8_0 --
 // Unit = 4 blocks of 32.  Lane c: block k = c/2 of the unit, half c%2.
 struct Q80 {

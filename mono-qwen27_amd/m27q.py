@@ -17,10 +17,10 @@ ROOT = os.path.dirname(PKG_DIR)
 LIB_PATH = os.path.join(PKG_DIR, "libm27q.so")
 HEADER = os.path.join(ROOT, "include", "m27q.h")
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 0, 1, 8, 12, 13, 14, 23
 GGUF, TILED = 0, 1
-BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
 
 STATUS = {0: "M27Q_OK", 1: "M27Q_ERR_NULL", 2: "M27Q_ERR_SHAPE", 3: "M27Q_ERR_TYPE",
           4: "M27Q_ERR_LAYOUT", 5: "M27Q_ERR_SCRATCH", 6: "M27Q_ERR_RANGE", 7: "M27Q_ERR_HIP"}

@@ -22,6 +22,7 @@ size_t ora_type_size(int type) {
         case ORA_Q5_K: return 176;
         case ORA_Q6_K: return 210;
         case ORA_Q8_K: return 292;
+        case ORA_IQ4_XS: return 136;
         default: return 0;
     }
 }
@@ -31,7 +32,7 @@ int ora_block_elems(int type) {
     switch (type) {
         case ORA_F32: case ORA_F16: return 1;
         case ORA_Q8_0: return 32;
-        case ORA_Q4_K: case ORA_Q5_K: case ORA_Q6_K: case ORA_Q8_K: return 256;
+        case ORA_Q4_K: case ORA_Q5_K: case ORA_Q6_K: case ORA_Q8_K: case ORA_IQ4_XS: return 256;
         default: return 0;
     }
 }
@@ -197,6 +198,30 @@ void ora_dequant_row_q8_0(const void *blocks, float *y, int64_t k) {
     }
 }
 
+const int8_t ora_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* 6-bit scale of 32-group j: 4 bits from scales_l, 2 from scales_h (exec:1004). */
+static int iq4xs_ls(const ora_block_iq4_xs *b, int j) {
+    return ((b->scales_l[j / 2] >> (4 * (j % 2))) & 0x0f) | (((b->scales_h >> (2 * j)) & 3) << 4);
+}
+
+/* ggml's dequantize_row_iq4_xs semantics (exec:992-1011 is the reference's
+ * fp32 form): y[32j + i] = (d (ls_j - 32)) kv[qs[16j + i] & 15],
+ * y[32j + 16 + i] = (d (ls_j - 32)) kv[qs[16j + i] >> 4]. */
+void ora_dequant_row_iq4_xs(const void *blocks, float *y, int64_t k) {
+    const ora_block_iq4_xs *x = (const ora_block_iq4_xs *)blocks;
+    for (int64_t b = 0; b < k / 256; ++b) {
+        const float d = ora_fp16_to_fp32(x[b].d);
+        for (int j = 0; j < 8; ++j) {
+            const float dl = d * (float)(iq4xs_ls(&x[b], j) - 32);
+            const uint8_t *q = x[b].qs + 16 * j;
+            for (int i = 0; i < 16; ++i) y[32 * j + i] = dl * (float)ora_kvalues_iq4nl[q[i] & 15];
+            for (int i = 0; i < 16; ++i) y[32 * j + 16 + i] = dl * (float)ora_kvalues_iq4nl[q[i] >> 4];
+        }
+        y += 256;
+    }
+}
+
 int ora_dequant_rows(int type, const void *w, int rb, int rc, float *y) {
     const int be = ora_block_elems(type);
     const size_t ts = ora_type_size(type);
@@ -210,6 +235,7 @@ int ora_dequant_rows(int type, const void *w, int rb, int rc, float *y) {
             case ORA_Q5_K: ora_dequant_row_q5_K(row, yr, k); break;
             case ORA_Q6_K: ora_dequant_row_q6_K(row, yr, k); break;
             case ORA_Q8_0: ora_dequant_row_q8_0(row, yr, k); break;
+            case ORA_IQ4_XS: ora_dequant_row_iq4_xs(row, yr, k); break;
             case ORA_F16: ora_fp16_to_fp32_n((const uint16_t *)row, yr, (size_t)k); break;
             case ORA_F32: memcpy(yr, row, (size_t)k * 4); break;
             default: return -1;
@@ -356,6 +382,41 @@ void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k) {
     }
 }
 
+/* IQ4_XS generator: a per-block d from the largest group amax, per-group 6-bit
+ * scales, nearest table entry per weight. */
+void ora_quantize_row_iq4_xs(const float *x, void *blocks, int64_t k) {
+    ora_block_iq4_xs *y = (ora_block_iq4_xs *)blocks;
+    for (int64_t b = 0; b < k / 256; ++b, x += 256) {
+        float amax[8], big = 0.f;
+        for (int j = 0; j < 8; ++j) {
+            amax[j] = 0.f;
+            for (int i = 0; i < 32; ++i) amax[j] = fmaxf(amax[j], fabsf(x[32 * j + i]));
+            big = fmaxf(big, amax[j]);
+        }
+        /* group scale s_j = amax_j / 127 = d (ls_j - 32), ls_j in [33, 63] */
+        const uint16_t dh = ora_fp32_to_fp16(big / 127.f / 31.f);
+        const float d = ora_fp16_to_fp32(dh);
+        memset(&y[b], 0, sizeof(y[b]));
+        y[b].d = dh;
+        for (int j = 0; j < 8; ++j) {
+            const int ls = d > 0.f ? clampi((int)lrintf(amax[j] / 127.f / d) + 32, 0, 63) : 32;
+            y[b].scales_l[j / 2] |= (uint8_t)((ls & 15) << (4 * (j % 2)));
+            y[b].scales_h |= (uint16_t)(((ls >> 4) & 3) << (2 * j));
+            const float dl = d * (float)(ls - 32);
+            for (int i = 0; i < 32; ++i) {
+                int best = 0;
+                float be = INFINITY;
+                for (int t = 0; t < 16; ++t) {
+                    const float e = fabsf(dl * (float)ora_kvalues_iq4nl[t] - x[32 * j + i]);
+                    if (e < be) { be = e; best = t; }
+                }
+                uint8_t *q = &y[b].qs[16 * j + (i & 15)];
+                *q |= (uint8_t)(i < 16 ? best : best << 4);
+            }
+        }
+    }
+}
+
 void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k) {
     ora_block_q8_0 *y = (ora_block_q8_0 *)blocks;
     for (int64_t i = 0; i < k / 32; ++i, x += 32) {
@@ -487,6 +548,23 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
                 nrm += fabs(t);
             }
         }
+    } else if (type == ORA_IQ4_XS) {
+        /* per 32-group j: d (ls_j - 32) dx_j sum(kv[q] q8) (exec:647-671) */
+        const ora_block_iq4_xs *w = (const ora_block_iq4_xs *)wrow;
+        for (int b = 0; b < rb; ++b) {
+            const double dw = ora_fp16_to_fp32(w[b].d);
+            for (int j = 0; j < 8; ++j) {
+                int sumi = 0;
+                for (int i = 0; i < 16; ++i) {
+                    const uint8_t qb = w[b].qs[16 * j + i];
+                    sumi += ora_kvalues_iq4nl[qb & 15] * q[256 * b + 32 * j + i];
+                    sumi += ora_kvalues_iq4nl[qb >> 4] * q[256 * b + 32 * j + 16 + i];
+                }
+                const double t = dw * (iq4xs_ls(&w[b], j) - 32) * (double)d[8 * b + j] * sumi;
+                acc += t;
+                nrm += fabs(t);
+            }
+        }
     } else if (type == ORA_Q8_0) {
         const ora_block_q8_0 *w = (const ora_block_q8_0 *)wrow;
         for (int b = 0; b < rb; ++b) {
@@ -506,7 +584,8 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
 int ora_gemv_act(int type, const void *w, int rb, int rc, const int8_t *q, const float *d,
                  const uint32_t *s, double *y, double *norm) {
     const size_t ts = ora_type_size(type);
-    if (!ts || (type != ORA_Q4_K && type != ORA_Q5_K && type != ORA_Q6_K && type != ORA_Q8_0)) return -1;
+    if (!ts || (type != ORA_Q4_K && type != ORA_Q5_K && type != ORA_Q6_K && type != ORA_Q8_0 && type != ORA_IQ4_XS))
+        return -1;
     for (int r = 0; r < rc; ++r)
         y[r] = ora_dot_act(type, (const uint8_t *)w + (size_t)r * rb * ts, rb, q, d, s, norm ? norm + r : NULL);
     return 0;
@@ -635,6 +714,36 @@ float ora_ref_vec_dot_q5_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int 
                 sumf_m += d8 * (float)(dot2 * m[i]);
             }
             total += ora_fp16_to_fp32(bq->d) * sumf_d - ora_fp16_to_fp32(bq->dmin) * sumf_m;
+        }
+    }
+    return total;
+}
+
+/* exec:647-671 (vec_dot_iq4_xs_q8_1): thread share iqs in {0,4,..,28}, each
+ * covering 32-group iqs/4 through the 16-entry table (get_int_from_table_16). */
+float ora_ref_vec_dot_iq4_xs_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb) {
+    const ora_block_iq4_xs *w = (const ora_block_iq4_xs *)wrow;
+    float total = 0.f;
+    for (int kbx = 0; kbx < rb; ++kbx) {
+        const ora_block_iq4_xs *bq = w + kbx;
+        const ora_block_q8_1 *b8 = xq + 8 * kbx;
+        for (int iqs = 0; iqs < 32; iqs += 4) {
+            int sumi = 0;
+            for (int j = 0; j < 4; ++j) {
+                const int aux = load_i32(bq->qs + 4 * (iqs + j));
+                int vx = 0, vy = 0;
+                for (int t = 0; t < 4; ++t) {
+                    vx |= (ora_kvalues_iq4nl[(aux >> (8 * t)) & 15] & 0xff) << (8 * t);
+                    vy |= (ora_kvalues_iq4nl[(aux >> (8 * t + 4)) & 15] & 0xff) << (8 * t);
+                }
+                const int u0 = load_i32(b8[iqs / 4].qs + 4 * j), u1 = load_i32(b8[iqs / 4].qs + 4 * (j + 4));
+                sumi = dp4(vx, u0, sumi);
+                sumi = dp4(vy, u1, sumi);
+            }
+            const int ls = ((bq->scales_l[iqs / 8] >> (iqs & 4)) & 15) | (((bq->scales_h >> (iqs / 2)) & 3) << 4);
+            sumi *= ls - 32;
+            const float d = ora_fp16_to_fp32(bq->d) * ora_fp16_to_fp32(b8[iqs / 4].d);
+            total += d * (float)sumi;
         }
     }
     return total;

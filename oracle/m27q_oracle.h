@@ -30,6 +30,9 @@
  *                         (ora_ref_vec_dot_q6_K_q8_1, exec:586-628) with one-hot
  *                         activations, plus single-bit known answers.
  *   ora_dequant_row_q8_0  the reference's dp4a formulation (exec:535-580).
+ *   ora_dequant_row_iq4_xs the reference's dp4a formulation (exec:647-671) with
+ *                         one-hot activations, and hand-set single blocks whose
+ *                         values are the table entries times d (ls - 32).
  *   ora_quant_act         an independent numpy restatement of the rule (float32
  *                         divide / reciprocal / multiply, round half away in float64),
  *                         and closed-form properties (|q|<=127, the max maps to +-127,
@@ -54,12 +57,17 @@ extern "C" {
 #endif
 
 /* ggml type ids (include/mono27b_gguf.h:27-43 in the reference). */
-enum { ORA_F32 = 0, ORA_F16 = 1, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q5_K = 13, ORA_Q6_K = 14, ORA_Q8_K = 15 };
+enum { ORA_F32 = 0, ORA_F16 = 1, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q5_K = 13, ORA_Q6_K = 14, ORA_Q8_K = 15,
+       ORA_IQ4_XS = 23 };
 
 /* GGUF block layouts (exec:18-23, :25-28, :38-42, :57-62). */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } ora_block_q4_K;
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } ora_block_q5_K; /* exec:30-36 */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } ora_block_q6_K;
+/* exec:44-49: f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128] (136 B, 8-byte aligned in a row) */
+typedef struct { uint16_t d, scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } ora_block_iq4_xs;
+/* The IQ4_NL / IQ4_XS value table (exec:51-55). */
+extern const int8_t ora_kvalues_iq4nl[16];
 typedef struct { uint16_t d; int8_t qs[32]; } ora_block_q8_0;
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } ora_block_q8_K;
 /* The reference's activation block (exec:65-71): half2 {d, sum(x)} + 32 codes. */
@@ -80,6 +88,7 @@ void ora_dequant_row_q4_K(const void *blocks, float *y, int64_t k);
 void ora_dequant_row_q5_K(const void *blocks, float *y, int64_t k);
 void ora_dequant_row_q6_K(const void *blocks, float *y, int64_t k);
 void ora_dequant_row_q8_0(const void *blocks, float *y, int64_t k);
+void ora_dequant_row_iq4_xs(const void *blocks, float *y, int64_t k);
 /* rc rows of rb blocks each, GGUF row-major; F16/F32 rows of rb elements. */
 int  ora_dequant_rows(int type, const void *w, int rb, int rc, float *y);
 
@@ -88,6 +97,7 @@ void ora_quantize_row_q4_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q5_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q6_K(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k);
+void ora_quantize_row_iq4_xs(const float *x, void *blocks, int64_t k);
 
 /* Activation format of the MI355X path: per 32 values, int8 codes, an fp32
  * scale d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0 (IEEE divide),
@@ -115,6 +125,7 @@ float ora_ref_vec_dot_q4_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int 
 float ora_ref_vec_dot_q5_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 float ora_ref_vec_dot_q6_K_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 float ora_ref_vec_dot_q8_0_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
+float ora_ref_vec_dot_iq4_xs_q8_1(const void *wrow, const ora_block_q8_1 *xq, int rb);
 
 /* ggml CPU path restatement (parity unpinned; CPU baseline). */
 void  ora_quantize_row_q8_K(const float *x, void *y, int64_t k);

@@ -16,9 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libm27q_oracle.so")
 REF_LIB_PATH = os.path.join(HERE, "_ref", "libofficial_dequant.so")
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 8, 12, 13, 14, 15
-TYPE_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
-BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, IQ4_XS = 0, 1, 8, 12, 13, 14, 15, 23
+TYPE_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, IQ4_XS: 136}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, IQ4_XS: 256}
 
 _lib = None
 
@@ -42,6 +42,7 @@ def lib() -> C.CDLL:
             "ora_quantize_row_q5_K": (None, [P, P, I64]),
             "ora_quantize_row_q6_K": (None, [P, P, I64]),
             "ora_quantize_row_q8_0": (None, [P, P, I64]),
+            "ora_quantize_row_iq4_xs": (None, [P, P, I64]),
             "ora_quant_act": (None, [P, I64, P, P, P]),
             "ora_quant_act_gated": (None, [P, P, I64, P, P, P]),
             "ora_dot_act": (D, [I, P, I, P, P, P, P]),
@@ -52,6 +53,7 @@ def lib() -> C.CDLL:
             "ora_ref_vec_dot_q5_K_q8_1": (C.c_float, [P, P, I]),
             "ora_ref_vec_dot_q6_K_q8_1": (C.c_float, [P, P, I]),
             "ora_ref_vec_dot_q8_0_q8_1": (C.c_float, [P, P, I]),
+            "ora_ref_vec_dot_iq4_xs_q8_1": (C.c_float, [P, P, I]),
             "ora_quantize_row_q8_K": (None, [P, P, I64]),
             "ora_quantize_row_q8_0_act": (None, [P, P, I64]),
             "ora_gemv_cpu": (I, [I, P, I, I, P, P, I]),
@@ -104,7 +106,7 @@ def quantize(type_: int, w: np.ndarray) -> np.ndarray:
         return fp32_to_fp16(w).view(np.uint8).reshape(rc, k * 2).copy()
     out = np.empty((rc, row_bytes(type_, k)), np.uint8)
     fn = {Q4_K: lib().ora_quantize_row_q4_K, Q5_K: lib().ora_quantize_row_q5_K, Q6_K: lib().ora_quantize_row_q6_K,
-          Q8_0: lib().ora_quantize_row_q8_0}[type_]
+          Q8_0: lib().ora_quantize_row_q8_0, IQ4_XS: lib().ora_quantize_row_iq4_xs}[type_]
     fn(_p(w), _p(out), w.size)  # rows are contiguous: one call quantizes them all
     return out
 
@@ -189,7 +191,7 @@ def ref_vec_dot_q8_1(type_: int, wrow: np.ndarray, xq: np.ndarray, rb: int) -> f
     wrow = np.ascontiguousarray(wrow)
     fn = {Q4_K: lib().ora_ref_vec_dot_q4_K_q8_1, Q5_K: lib().ora_ref_vec_dot_q5_K_q8_1,
           Q6_K: lib().ora_ref_vec_dot_q6_K_q8_1,
-          Q8_0: lib().ora_ref_vec_dot_q8_0_q8_1}[type_]
+          Q8_0: lib().ora_ref_vec_dot_q8_0_q8_1, IQ4_XS: lib().ora_ref_vec_dot_iq4_xs_q8_1}[type_]
     return float(fn(_p(wrow), xq.ctypes.data, rb))
 
 

@@ -31,7 +31,7 @@ def test_status_strings(m27q):
 
 def test_row_size_matches_gguf_block_table(m27q, ora):
     # src/mono27b_gguf.cpp:375-382: whole blocks only, 0 otherwise
-    for t in (m27q.Q4_K, m27q.Q5_K, m27q.Q6_K, m27q.Q8_0, m27q.F16, m27q.F32):
+    for t in (m27q.Q4_K, m27q.Q5_K, m27q.Q6_K, m27q.Q8_0, m27q.IQ4_XS, m27q.F16, m27q.F32):
         be, bb = m27q.BLOCK_ELEMS[t], m27q.BLOCK_BYTES[t]
         assert m27q.row_size(t, 5120) == 5120 // be * bb
         assert m27q.row_size(t, 0) == 0
@@ -41,7 +41,7 @@ def test_row_size_matches_gguf_block_table(m27q, ora):
     assert m27q.row_size(99, 256) == 0
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
 @pytest.mark.parametrize("rb,rc", [(1, 1), (3, 13), (20, 64), (5, 9)])
 def test_repack_roundtrip(m27q, type_name, rb, rc):
     t = getattr(m27q, type_name)
@@ -73,6 +73,12 @@ def test_tiled_layout_offsets(m27q):
     assert np.array_equal(tiled[unit + 16 * i: unit + 16 * i + 16], raw[r, b, :16])
     assert np.array_equal(tiled[unit + 128 + 128 * i: unit + 256 + 128 * i], raw[r, b, 48:])
     assert np.array_equal(tiled[unit + 1152 + 32 * i: unit + 1184 + 32 * i], raw[r, b, 16:48])
+    t = m27q.IQ4_XS
+    raw = RNG.integers(0, 256, (rc, rb, 136), dtype=np.uint8)
+    tiled = m27q.repack(t, rb, rc, raw.reshape(-1))
+    unit = ((r // 8) * rb + b) * 1088
+    assert np.array_equal(tiled[unit + 128 * i: unit + 128 * i + 128], raw[r, b, 8:])
+    assert np.array_equal(tiled[unit + 1024 + 8 * i: unit + 1032 + 8 * i], raw[r, b, :8])
     t = m27q.Q6_K
     raw = RNG.integers(0, 256, (rc, rb, 210), dtype=np.uint8)
     tiled = m27q.repack(t, rb, rc, raw.reshape(-1))

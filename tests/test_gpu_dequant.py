@@ -7,7 +7,7 @@ from test_oracle import random_blocks
 
 pytestmark = pytest.mark.gpu
 
-TYPES = ["Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+TYPES = ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"]
 
 
 @pytest.mark.parametrize("type_name", TYPES)

@@ -19,6 +19,8 @@ SHAPES = {  # (type, rows, K)
     "q4k_o": ("Q4_K", 5120, 6144),
     "q5k_gate": ("Q5_K", 6144, 5120),
     "q5k_small": ("Q5_K", 24, 768),
+    "iq4_gate": ("IQ4_XS", 6144, 5120),
+    "iq4_small": ("IQ4_XS", 24, 768),
     "q6k_down": ("Q6_K", 5120, 17408),
     "q6k_small": ("Q6_K", 24, 768),
     "q80_2048": ("Q8_0", 2048, 2048),
@@ -162,7 +164,7 @@ def test_multi_matches_single(m27q, ora, dev):
         assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K"])
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "IQ4_XS"])
 def test_ffn_swiglu(m27q, ora, dev, type_name):
     import torch
     t = getattr(m27q, type_name)
@@ -199,7 +201,8 @@ def check_swiglu(ora, t, gb, ub, rc, q, d, s, y):
     assert (err <= tol).all(), (np.flatnonzero(err > tol)[:5], err.max())
 
 
-@pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged", "q5k_gate", "q5k_small"])
+@pytest.mark.parametrize("shape", ["q4k_ffn", "q6k_down", "q80_down", "q4k_small", "q80_ragged", "q5k_gate", "q5k_small",
+                                   "iq4_gate", "iq4_small"])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_matvec_f32_vs_fp64(m27q, ora, dev, shape, layout):
     import torch
@@ -238,7 +241,7 @@ def test_matvec_dense(m27q, ora, dev, type_name):
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 5120, 6144), ("Q4_K", 17408, 5120),
-                                             ("Q8_0", 2048, 6144), ("Q5_K", 5120, 6144)])
+                                             ("Q8_0", 2048, 6144), ("Q5_K", 5120, 6144), ("IQ4_XS", 5120, 6144)])
 def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so at
     shapes where both input forms launch the same workgroup shape the product

@@ -20,6 +20,9 @@ CASES = [  # type, rows, K, M, layout
     ("Q8_0", 2048, 6144, 4, 1),
     # Q5_K on each path: few-token GEMV, MFMA, GGUF VALU
     ("Q5_K", 6144, 5120, 2, 1), ("Q5_K", 6144, 5120, 16, 1), ("Q5_K", 40, 512, 9, 1), ("Q5_K", 40, 512, 3, 0),
+    # IQ4_XS likewise
+    ("IQ4_XS", 6144, 5120, 2, 1), ("IQ4_XS", 6144, 5120, 16, 1), ("IQ4_XS", 40, 512, 9, 1),
+    ("IQ4_XS", 40, 512, 3, 0),
 ]
 
 

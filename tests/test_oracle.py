@@ -34,12 +34,12 @@ def random_blocks(ora, type_, nblocks, rng=RNG):
         b[:, 2:4] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
     elif type_ == ora.Q6_K:
         b[:, 208:210] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
-    elif type_ == ora.Q8_0:
+    elif type_ in (ora.Q8_0, ora.IQ4_XS):
         b[:, 0:2] = f16(nblocks).view(np.uint8).reshape(nblocks, 2)
     # a few subnormal / zero scales
     sub = np.array([0x0001, 0x03ff, 0x8001, 0x0000, 0x8000], np.uint16).view(np.uint8).reshape(5, 2)
     for i in range(min(5, nblocks)):
-        off = {ora.Q4_K: 0, ora.Q5_K: 0, ora.Q6_K: 208, ora.Q8_0: 0}[type_]
+        off = {ora.Q4_K: 0, ora.Q5_K: 0, ora.Q6_K: 208, ora.Q8_0: 0, ora.IQ4_XS: 0}[type_]
         b[i, off:off + 2] = sub[i]
     return b
 
@@ -84,7 +84,7 @@ def test_q4k_matches_reference_c_build(ora):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
 def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
     """x = 127 e_j quantizes to d = 1, code 127 at j: the reference's dp4a dot then
     returns 127 * W[j] (rounded once or twice), which pins every position's
@@ -105,6 +105,8 @@ def test_dequant_matches_reference_vecdot_formulation(ora, type_name):
             return 127.0 * 63 * (qmax * f16(b, 0) + f16(b, 2))
         if t == ora.Q6_K:
             return 127.0 * 128 * 32 * f16(b, 208)
+        if t == ora.IQ4_XS:
+            return 127.0 * 127 * 32 * f16(b, 0)
         return 127.0 * 128 * f16(b, 0)
 
     for trial in range(3):
@@ -182,7 +184,31 @@ def scale_min(q, j):
     return (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
 
 
-@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
+def test_iq4xs_hand_set_block(ora):
+    """d = 1, group scales ls_j = 32 + j + 1 (6 bits over scales_l / scales_h),
+    index pattern (i + j) % 16: every value is (j + 1) kv[(i + j) % 16], with kv the
+    table of exec:51-55, low nibbles at positions 0..15 of a group, high 16..31."""
+    kv = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)  # d = 1.0
+    sh = 0
+    for j in range(8):
+        ls = 32 + j + 1
+        blk[4 + j // 2] |= (ls & 15) << (4 * (j % 2))
+        sh |= ((ls >> 4) & 3) << (2 * j)
+        for i in range(16):
+            blk[8 + 16 * j + i] = ((i + j) % 16) | (((i + j + 5) % 16) << 4)
+    blk[2:4] = np.array([sh], np.uint16).view(np.uint8)
+    y = ora.dequant(ora.IQ4_XS, blk, 1, 1)[0]
+    want = np.zeros(256, np.float32)
+    for j in range(8):
+        for i in range(16):
+            want[32 * j + i] = (j + 1) * kv[(i + j) % 16]
+            want[32 * j + 16 + i] = (j + 1) * kv[(i + j + 5) % 16]
+    assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
 def test_int_dot_oracle_vs_numpy_bruteforce(ora, type_name):
     t = getattr(ora, type_name)
     be = ora.BLOCK_ELEMS[t]
