@@ -235,6 +235,20 @@ M27Q_API size_t m27q_topk_scratch_bytes(int n, int k);
 M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, float *val, void *scratch,
                                size_t scratch_bytes, hipStream_t stream);
 
+/* On-device token choice from m27q_topk's candidates (idx/val in rank order,
+ * 1 <= k <= 64), the steps of sample() (src/mono27b_chat.cpp:203-270) after its
+ * top-k: temperature <= 0 gives idx[0] (the argmax, first index on ties);
+ * otherwise p_i = expf((val_i - val_0) / temperature), normalized; candidates
+ * with p_i < p_0 * min_p are dropped; top_p < 1 keeps the shortest prefix whose
+ * running sum reaches top_p; the token is the first candidate whose running sum
+ * reaches u * (sum of the kept p).  u is a device float in [0, 1), token a
+ * device int32: per-step values stay on the device, so the step can be replayed
+ * as a graph.  Banned tokens: the caller sets their logits to -inf before
+ * m27q_topk, as sample() does on its copy (:206-211).  Sums run in candidate
+ * order, as the reference's loop. */
+M27Q_API m27q_status m27q_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p,
+                                 float top_p, const float *u, int32_t *token, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

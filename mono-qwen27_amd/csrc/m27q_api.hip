@@ -4,6 +4,7 @@
 // returns a status without touching the device (the reference's launchers
 // return silently instead, exec:2034, :2056-2059).
 #include <climits>
+#include <cmath>
 
 #include "m27q_internal.h"
 
@@ -381,6 +382,15 @@ M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, 
     if (scratch_bytes < topk_scratch_bytes(n)) return M27Q_ERR_SCRATCH;
     if (!aligned(scratch, 8)) return M27Q_ERR_LAYOUT;
     return hip_status(launch_topk(logits, n, k, idx, val, scratch, stream));
+}
+
+M27Q_API m27q_status m27q_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p,
+                                 float top_p, const float *u, int32_t *token, hipStream_t stream) {
+    if (!idx || !val || !u || !token) return M27Q_ERR_NULL;
+    if (k < 1 || k > kMaxTopK) return M27Q_ERR_RANGE;
+    if (!(min_p >= 0.f) || !(top_p > 0.f) || std::isnan(temperature)) return M27Q_ERR_RANGE;
+    if (!aligned(idx, 4) || !aligned(val, 4) || !aligned(u, 4) || !aligned(token, 4)) return M27Q_ERR_LAYOUT;
+    return hip_status(launch_sample(idx, val, k, temperature, min_p, top_p, u, token, stream));
 }
 
 }  // extern "C"

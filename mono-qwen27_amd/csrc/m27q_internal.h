@@ -63,6 +63,8 @@ hipError_t launch_gather(const GatherParams &p, hipStream_t s);
 
 size_t topk_scratch_bytes(int n);
 hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, void *scratch, hipStream_t s);
+hipError_t launch_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p,
+                         const float *u, int32_t *token, hipStream_t s);
 
 struct MatmulParams {
     const uint8_t *W;

@@ -306,6 +306,72 @@ __global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__re
     }
 }
 
+// Sampling from the top-k candidates, in the steps and order of sample()
+// (src/mono27b_chat.cpp:203-270) after its top-k: probabilities
+// expf((v_i - v_0) / T) computed per lane, then one lane runs the sum, the
+// normalization, the min_p and top_p cuts and the pick in candidate order, so
+// the float sums round as the reference's sequential loop does.
+__global__ __launch_bounds__(kWave) void k_sample(const int32_t *__restrict__ idx, const float *__restrict__ val,
+                                                  int k, float temperature, float min_p, float top_p,
+                                                  const float *__restrict__ u, int32_t *__restrict__ token) {
+    __shared__ float p[kTopkMaxK];
+    __shared__ int kept[kTopkMaxK];
+    const int lane = (int)threadIdx.x;
+    const int best = idx[0];
+    if (!(temperature > 0.f)) {
+        if (lane == 0) *token = best;
+        return;
+    }
+    if (lane < k) p[lane] = expf((val[lane] - val[0]) / temperature);
+    __syncthreads();
+    if (lane != 0) return;
+    float sum = 0.f;
+    for (int i = 0; i < k; ++i) sum += p[i];
+    if (!(sum > 0.f) || !isfinite(sum)) {
+        *token = best;
+        return;
+    }
+    for (int i = 0; i < k; ++i) p[i] /= sum;
+    // min_p: drop candidates below p_0 * min_p (kept in order); p_0 itself
+    // always stays unless min_p > 1, and then the pick falls back to best.
+    const float thresh = p[0] * min_p;
+    int n = 0;
+    for (int i = 0; i < k; ++i)
+        if (!(p[i] < thresh)) kept[n++] = i;
+    if (n == 0) {
+        *token = best;
+        return;
+    }
+    if (top_p < 1.f) {
+        float acc = 0.f;
+        for (int i = 0; i < n; ++i) {
+            acc += p[kept[i]];
+            if (acc >= top_p) {
+                n = i + 1;
+                break;
+            }
+        }
+    }
+    float total = 0.f;
+    for (int i = 0; i < n; ++i) total += p[kept[i]];
+    const float pick = *u * total;
+    float run = 0.f;
+    for (int i = 0; i < n; ++i) {
+        run += p[kept[i]];
+        if (pick <= run) {
+            *token = idx[kept[i]];
+            return;
+        }
+    }
+    *token = idx[kept[n - 1]];
+}
+
+hipError_t launch_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p,
+                         const float *u, int32_t *token, hipStream_t s) {
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(kWave), 0, s, idx, val, k, temperature, min_p, top_p, u, token);
+    return hipGetLastError();
+}
+
 // Values per chunk workgroup: 1024 for the vocab (243 chunks), doubled until
 // the chunk count fits.
 static int topk_chunk(int n) {

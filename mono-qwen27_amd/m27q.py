@@ -63,6 +63,7 @@ _SIGS = {
     "m27q_embed_token": (_I, [C.POINTER(WeightDesc), C.c_int32, _P, _P]),
     "m27q_topk_scratch_bytes": (_SZ, [_I, _I]),
     "m27q_topk": (_I, [_P, _I, _I, _P, _P, _P, _SZ, _P]),
+    "m27q_sample": (_I, [_P, _P, _I, C.c_float, C.c_float, C.c_float, _P, _P, _P]),
 }
 
 _lib = None
@@ -274,6 +275,12 @@ def embed_token(w: Weight, token_id: int, out, stream=None) -> None:
 
 def topk_scratch_bytes(n: int, k: int) -> int:
     return lib().m27q_topk_scratch_bytes(n, k)
+
+
+def sample(idx, val, k: int, temperature: float, min_p: float, top_p: float, u, token, stream=None) -> None:
+    """token[0] <- the candidate sample() picks for the uniform u[0] (device tensors)."""
+    check(lib().m27q_sample(_ptr(idx), _ptr(val), k, temperature, min_p, top_p, _ptr(u), _ptr(token),
+                            _stream(stream)), "m27q_sample")
 
 
 def topk(logits, k: int, idx, val, scratch, stream=None) -> None:

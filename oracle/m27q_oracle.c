@@ -960,6 +960,43 @@ static int cmp_vi(const void *pa, const void *pb) {
     return (a->i > b->i) - (a->i < b->i);
 }
 
+int ora_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p, float u) {
+    if (!(temperature > 0.f)) return idx[0];
+    float p[64];
+    int kept[64];
+    float sum = 0.f;
+    for (int i = 0; i < k; ++i) {
+        p[i] = expf((val[i] - val[0]) / temperature);
+        sum += p[i];
+    }
+    if (!(sum > 0.f) || !isfinite(sum)) return idx[0];
+    for (int i = 0; i < k; ++i) p[i] /= sum;
+    const float thresh = p[0] * min_p;
+    int n = 0;
+    for (int i = 0; i < k; ++i)
+        if (!(p[i] < thresh)) kept[n++] = i;
+    if (n == 0) return idx[0];
+    if (top_p < 1.f) {
+        float acc = 0.f;
+        for (int i = 0; i < n; ++i) {
+            acc += p[kept[i]];
+            if (acc >= top_p) {
+                n = i + 1;
+                break;
+            }
+        }
+    }
+    float total = 0.f;
+    for (int i = 0; i < n; ++i) total += p[kept[i]];
+    const float pick = u * total;
+    float run = 0.f;
+    for (int i = 0; i < n; ++i) {
+        run += p[kept[i]];
+        if (pick <= run) return idx[kept[i]];
+    }
+    return idx[kept[n - 1]];
+}
+
 int ora_topk(const float *v, int n, int k, int32_t *idx, float *val) {
     if (n <= 0 || k <= 0 || k > n) return -1;
     vi_pair *p = (vi_pair *)malloc((size_t)n * sizeof *p);

@@ -40,6 +40,10 @@
  *   ora_dot_act           brute force (dequantized weights x dequantized activation
  *                         in fp64) on small shapes, and one-hot / zero inputs.
  *   ora_topk              numpy lexsort on the same values.
+ *   ora_sample            closed-form properties: temperature <= 0 and u = 0 give
+ *                         the first candidate, top_p -> 0 and min_p = 1 keep only
+ *                         it, and over a fine grid of u the share of each token
+ *                         equals its kept probability.
  *   ggml q8_K routines    PARITY UNPINNED: ggml itself (ref/llama.cpp) is absent from
  *                         the reference checkout and no version is pinned.  They are a
  *                         restatement of ggml's published generic C path, used only as
@@ -136,6 +140,12 @@ float ora_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy);
 /* y[r] for r in [0, rc), rows split over nthreads pthreads.  xq is the
  * activation quantized to q8_K (K-quants) or q8_0 (Q8_0). */
 int ora_gemv_cpu(int type, const void *w, int rb, int rc, const void *xq, float *y, int nthreads);
+
+/* sample() (src/mono27b_chat.cpp:203-270) after its top-k, on candidates
+ * idx/val in rank order: temperature <= 0 -> idx[0]; softmax at the
+ * temperature (expf, float32, sums in candidate order), min_p and top_p cuts,
+ * pick = u * total, the first candidate whose running sum reaches it. */
+int ora_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p, float u);
 
 /* Exact top-k by (value desc, index asc); NaN ranks after every number. */
 int ora_topk(const float *v, int n, int k, int32_t *idx, float *val);

@@ -55,6 +55,7 @@ def lib() -> C.CDLL:
             "ora_ref_vec_dot_q8_0_q8_1": (C.c_float, [P, P, I]),
             "ora_ref_vec_dot_iq4_xs_q8_1": (C.c_float, [P, P, I]),
             "ora_quantize_row_q8_K": (None, [P, P, I64]),
+            "ora_sample": (I, [P, P, I, C.c_float, C.c_float, C.c_float, C.c_float]),
             "ora_quantize_row_q8_0_act": (None, [P, P, I64]),
             "ora_gemv_cpu": (I, [I, P, I, I, P, P, I]),
             "ora_topk": (I, [P, I, I, P, P]),
@@ -217,6 +218,12 @@ def gemv_cpu(type_: int, blocks: np.ndarray, rb: int, rc: int, xq: np.ndarray, n
 
 
 # ---------------------------------------------------------------- top-k --
+
+def sample(idx: np.ndarray, val: np.ndarray, temperature: float, min_p: float, top_p: float, u: float) -> int:
+    idx = np.ascontiguousarray(idx, np.int32)
+    val = np.ascontiguousarray(val, np.float32)
+    return int(lib().ora_sample(_p(idx), _p(val), idx.size, temperature, min_p, top_p, u))
+
 
 def topk(v: np.ndarray, k: int):
     v = np.ascontiguousarray(v, dtype=np.float32)

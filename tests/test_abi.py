@@ -193,4 +193,8 @@ def test_validation_gather_and_topk(m27q):
     assert L.m27q_topk(FAKE, 248320, 64, FAKE, FAKE, FAKE, 64, None) == 5
     assert L.m27q_topk(None, 10, 1, FAKE, FAKE, FAKE, 1 << 20, None) == 1
     assert m27q.topk_scratch_bytes(248320, 64) >= 64 * 8
+    assert L.m27q_sample(FAKE, FAKE, 0, 1.0, 0.05, 0.9, FAKE, FAKE, None) == 6
+    assert L.m27q_sample(FAKE, FAKE, 65, 1.0, 0.05, 0.9, FAKE, FAKE, None) == 6
+    assert L.m27q_sample(FAKE, FAKE, 40, 1.0, 0.05, 0.0, FAKE, FAKE, None) == 6
+    assert L.m27q_sample(None, FAKE, 40, 1.0, 0.05, 0.9, FAKE, FAKE, None) == 1
     assert m27q.topk_scratch_bytes(10, 11) == 0

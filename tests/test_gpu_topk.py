@@ -102,3 +102,28 @@ def test_vocab_scoring_full_size(m27q, ora, dev):
     want, nrm = ora.gemv_act(m27q.Q6_K, host, rb, rows.size, to_host(codes)[0], to_host(d)[0],
                              to_host(s)[0].view(np.uint32))
     assert (np.abs(lg[rows] - want) <= 1e-5 * nrm + 1e-30).all()
+
+
+@pytest.mark.parametrize("T,min_p,top_p", [(0.8, 0.05, 0.95), (1.0, 0.0, 1.0), (0.3, 0.1, 0.6), (0.0, 0.05, 0.95)])
+def test_sample_matches_oracle(m27q, ora, dev, T, min_p, top_p):
+    """m27q_sample on m27q_topk's candidates (k = 40, the reference's default
+    top_k) against the oracle's restatement of sample(), for a grid of u; u
+    values within 1e-5 of a pick boundary are skipped (expf may differ by an
+    ulp between the GPU and the host)."""
+    import torch
+    lg = (np.random.default_rng(4).standard_normal(248320) * 3).astype(np.float32)
+    k = 40
+    idx, val = run_topk(m27q, dev, lg, k)
+    di, dv = to_dev(idx, dev), to_dev(val, dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    checked = 0
+    say("sample", T, min_p, top_p)
+    for u in np.linspace(0.0, 0.999, 200, dtype=np.float32):
+        want = ora.sample(idx, val, T, min_p, top_p, float(u))
+        if u > 1e-5 and (ora.sample(idx, val, T, min_p, top_p, float(u) - 1e-5) != want or
+                         ora.sample(idx, val, T, min_p, top_p, float(u) + 1e-5) != want):
+            continue
+        m27q.sample(di, dv, k, T, min_p, top_p, to_dev(np.array([u], np.float32), dev), tok)
+        assert int(to_host(tok)[0]) == want, float(u)
+        checked += 1
+    assert checked > 150

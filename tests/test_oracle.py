@@ -306,3 +306,31 @@ def test_q8k_cpu_path_is_a_sane_approximation(ora):
         ref = ora.gemv_f64(t, w, rb, 32, x)
         scale = np.abs(ora.dequant(t, w, rb, 32)).sum(1) * np.abs(x).max()
         assert (np.abs(y - ref) <= 0.02 * scale).all()
+
+
+def test_sample_properties(ora):
+    """sample() after its top-k: first candidate for temperature <= 0, for u = 0,
+    for top_p -> 0 and for min_p = 1 (distinct values); over a fine grid of u
+    the share of each token equals its kept probability."""
+    rng = np.random.default_rng(11)
+    val = np.sort(rng.standard_normal(40).astype(np.float32))[::-1].copy()
+    idx = rng.permutation(1000)[:40].astype(np.int32)
+    assert ora.sample(idx, val, 0.0, 0.05, 0.95, 0.7) == idx[0]
+    assert ora.sample(idx, val, 0.8, 0.05, 0.95, 0.0) == idx[0]
+    assert ora.sample(idx, val, 0.8, 0.0, 1e-9, 0.99) == idx[0]
+    assert ora.sample(idx, val, 0.8, 1.0, 1.0, 0.99) == idx[0]
+    for T, min_p, top_p in ((0.8, 0.05, 0.95), (1.5, 0.0, 1.0), (0.3, 0.2, 0.5)):
+        p = np.exp((val.astype(np.float64) - val[0]) / T)
+        p /= p.sum()
+        keep = p >= p[0] * min_p
+        ks = np.flatnonzero(keep)
+        if top_p < 1:
+            c = np.cumsum(p[ks])
+            ks = ks[: int(np.searchsorted(c, top_p * (1 - 1e-6))) + 1]
+        q = p[ks] / p[ks].sum()
+        N = 20000
+        us = (np.arange(N) + 0.5) / N
+        got = np.array([ora.sample(idx, val, T, min_p, top_p, float(u)) for u in us])
+        for i, want in zip(ks, q):
+            assert abs((got == idx[i]).mean() - want) <= 2.0 / N + 1e-6
+        assert set(got) <= set(idx[ks])
