@@ -43,7 +43,8 @@ typedef enum m27q_status {
     M27Q_ERR_LAYOUT = 4,      /* unknown layout tag or misaligned buffer */
     M27Q_ERR_SCRATCH = 5,     /* scratch buffer smaller than required */
     M27Q_ERR_RANGE = 6,       /* token id out of range, or k > n */
-    M27Q_ERR_HIP = 7          /* the HIP launch itself failed */
+    M27Q_ERR_HIP = 7,         /* the HIP launch itself failed */
+    M27Q_ERR_IO = 8           /* a file could not be read or written, or is not a .m27b blob */
 } m27q_status;
 
 /* ggml type ids, as include/mono27b_gguf.h:27-43 numbers them. */
@@ -99,6 +100,17 @@ M27Q_API m27q_status m27q_repack(uint32_t ggml_type, uint32_t row_blocks, uint32
 /* TILED -> GGUF rows (the exact inverse of m27q_repack). */
 M27Q_API m27q_status m27q_unpack(uint32_t ggml_type, uint32_t row_blocks, uint32_t row_count,
                                  const void *tiled, void *gguf_rows);
+
+/* Re-tile a .m27b weight blob (include/mono27b_format.h:30-84) at pack time:
+ * out_path gets a copy of in_path in which every matrix entry of a type with
+ * a TILED form (whole GGUF rows) is re-tiled, its data_bytes updated and its
+ * reserved field set to M27Q_LAYOUT_TILED; tensors are 256-byte aligned in the
+ * file; the header, tokenizer section and all other tensors are copied.  The
+ * result passes the reference's mono27b_validate_blob_file and
+ * mono27b_read_weights_section.  Entries already tagged TILED are copied.
+ * Streams one tensor at a time.  Fills the role the reference's missing packer
+ * would have (the writer is src/mono27b_blob.cpp:378-438). */
+M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path);
 
 /* ------------------------------------------------------------------------
  * Activations

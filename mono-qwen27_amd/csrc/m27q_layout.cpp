@@ -118,6 +118,7 @@ M27Q_API const char *m27q_status_string(m27q_status s) {
         case M27Q_ERR_SCRATCH: return "scratch buffer too small";
         case M27Q_ERR_RANGE: return "index out of range";
         case M27Q_ERR_HIP: return "HIP launch failed";
+        case M27Q_ERR_IO: return "file read/write failed, or not a .m27b blob";
     }
     return "unknown status";
 }

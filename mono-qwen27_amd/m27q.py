@@ -23,7 +23,7 @@ BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS
 BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
 
 STATUS = {0: "M27Q_OK", 1: "M27Q_ERR_NULL", 2: "M27Q_ERR_SHAPE", 3: "M27Q_ERR_TYPE",
-          4: "M27Q_ERR_LAYOUT", 5: "M27Q_ERR_SCRATCH", 6: "M27Q_ERR_RANGE", 7: "M27Q_ERR_HIP"}
+          4: "M27Q_ERR_LAYOUT", 5: "M27Q_ERR_SCRATCH", 6: "M27Q_ERR_RANGE", 7: "M27Q_ERR_HIP", 8: "M27Q_ERR_IO"}
 
 
 class M27QError(RuntimeError):
@@ -44,6 +44,7 @@ _SIGS = {
     "m27q_weight_bytes": (_SZ, [_U32, _U32, _U32, _U32]),
     "m27q_repack": (_I, [_U32, _U32, _U32, _P, _P]),
     "m27q_unpack": (_I, [_U32, _U32, _U32, _P, _P]),
+    "m27q_retile_blob": (_I, [C.c_char_p, C.c_char_p]),
     "m27q_act_bytes": (_SZ, [_I, _I]),
     "m27q_act_d_offset": (_SZ, [_I, _I]),
     "m27q_act_s_offset": (_SZ, [_I, _I]),
@@ -116,6 +117,11 @@ def unpack(type_: int, rb: int, rc: int, tiled: np.ndarray) -> np.ndarray:
     out = np.empty(rc * rb * BLOCK_BYTES[type_], np.uint8)
     check(lib().m27q_unpack(type_, rb, rc, tiled.ctypes.data, out.ctypes.data), "m27q_unpack")
     return out
+
+
+def retile_blob(in_path: str, out_path: str) -> None:
+    """Copy a .m27b blob with its quantized matrices re-tiled (host, pack time)."""
+    check(lib().m27q_retile_blob(in_path.encode(), out_path.encode()), "m27q_retile_blob")
 
 
 def act_bytes(M: int, K: int) -> int:
