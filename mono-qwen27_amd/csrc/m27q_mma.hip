@@ -121,15 +121,18 @@ struct MmaQ4KT {
         // Software pipeline: the MFMAs of group j + 1 are issued before the
         // scale arithmetic of group j; the scheduling barrier keeps each group's
         // values local.
+        // The activation scales of group j + 1 are read from LDS one group
+        // ahead as well, so no group waits on its own LDS read.
         v4i c[RT];
 #pragma unroll
         for (int t = 0; t < RT; ++t) c[t] = mfma32(a[0], operand(f[t], 0), v4i{0, 0, 0, 0});
+        float4 dx = sl.dx(g0, q);
 #pragma unroll
         for (int j = 0; j < kGroups; ++j) {
             v4i cn[RT];
 #pragma unroll
             for (int t = 0; t < RT; ++t) cn[t] = j + 1 < kGroups ? mfma32(a[j + 1], operand(f[t], j + 1), v4i{0, 0, 0, 0}) : c[t];
-            const float4 dx = sl.dx(g0 + j, q);
+            const float4 dxn = j + 1 < kGroups ? sl.dx(g0 + j + 1, q) : dx;
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
                 const uint32_t scw = j < 4 ? scA[t] : scB[t];
@@ -138,6 +141,7 @@ struct MmaQ4KT {
                 for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(ws, f4(dx, e) * (float)c[t][e], acc[t][e]);
                 c[t] = cn[t];
             }
+            dx = dxn;
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -212,12 +216,13 @@ struct MmaQ6K {
             }
         };
         mm(0, c0, c1);
+        float4 dx = sl.dx(g0, q);  // one group ahead, as for Q4_K
 #pragma unroll
         for (int j = 0; j < kGroups; ++j) {
             v4i n0[RT], n1[RT];
             if (j + 1 < kGroups) mm(j + 1, n0, n1);
             const int h = j >> 2, r = j & 3;
-            const float4 dx = sl.dx(g0 + j, q);
+            const float4 dxn = j + 1 < kGroups ? sl.dx(g0 + j + 1, q) : dx;
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
                 const int s0 = sc_byte(f[t].sc, 8 * h + 2 * r), s1 = sc_byte(f[t].sc, 8 * h + 2 * r + 1);
@@ -231,6 +236,7 @@ struct MmaQ6K {
                     c1[t] = n1[t];
                 }
             }
+            dx = dxn;
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
