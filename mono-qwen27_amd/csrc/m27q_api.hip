@@ -148,9 +148,11 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
 
 // Small-M products for TILED weights: up to kMtMaxM tokens on the GEMV
 // streaming structure when their activations fit the LDS budget
-// (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).
+// (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).  Measured on the
+// Qwen-27B layer: 56 us against 63 at M = 2; from M = 3 on the MFMA kernel
+// with two row sets per tile is faster (63 against 75 us at M = 4).
 #ifndef M27Q_MT_MAXM
-#define M27Q_MT_MAXM 4
+#define M27Q_MT_MAXM 2
 #endif
 constexpr int kMtMaxM = M27Q_MT_MAXM;
 constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU

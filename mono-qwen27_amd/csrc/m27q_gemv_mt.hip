@@ -6,11 +6,9 @@
 // buffered and unconditional), and every loaded fragment is applied to MT
 // activation rows staged in LDS: the weight unpacking is shared by the tokens,
 // each token adds its own integer dots and scale terms, and no lane works on a
-// padding token unless M is not a multiple of MT.  The 16 x 16 MFMA tile, by
-// contrast, spends the same scale arithmetic on 16 token columns whatever M
-// is.  Measured on the Qwen-27B layer: 66 us against 115 us at M = 2, 103
-// against 118 at M = 4; at M = 8 the per-token dots make it no faster than
-// the MFMA kernel, which keeps M > 4.
+// padding token unless M is not a multiple of MT.  Its cost grows with the
+// per-token dots: on the Qwen-27B layer it takes 56 us at M = 2, against 63
+// for the MFMA kernel, which is faster from M = 3 on; it serves M <= 2.
 // No reference counterpart: the reference runs prefill and decode one token at
 // a time (src/mono27b_chat.cpp:399-403).
 #include <algorithm>
@@ -198,18 +196,12 @@ static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
     }
 }
 
-static int mt_of(int M) { return M <= 2 ? 2 : M <= 4 ? 4 : 8; }
-
-size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M) {
+size_t matmul_mt_lds_bytes(uint32_t type, int upr, int) {
     // the largest over the launch shapes the selection can return
-    const int mt = mt_of(M);
     auto one = [&](auto tag) -> size_t {
         using T = decltype(tag);
-        switch (mt) {
-            case 2: return std::max({mt_lds<T, Cfg41, 2>(upr), mt_lds<T, Cfg81, 2>(upr), mt_lds<T, Cfg42, 2>(upr), mt_lds<T, Cfg84, 2>(upr)});
-            case 4: return std::max({mt_lds<T, Cfg41, 4>(upr), mt_lds<T, Cfg81, 4>(upr), mt_lds<T, Cfg42, 4>(upr), mt_lds<T, Cfg84, 4>(upr)});
-            default: return std::max({mt_lds<T, Cfg41, 8>(upr), mt_lds<T, Cfg81, 8>(upr), mt_lds<T, Cfg42, 8>(upr), mt_lds<T, Cfg84, 8>(upr)});
-        }
+        return std::max({mt_lds<T, Cfg41, 2>(upr), mt_lds<T, Cfg81, 2>(upr), mt_lds<T, Cfg42, 2>(upr),
+                         mt_lds<T, Cfg84, 2>(upr)});
     };
     switch (type) {
         case kQ4_K: return one(Q4K{});
@@ -221,22 +213,14 @@ size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M) {
     }
 }
 
-template <class T>
-static hipError_t launch_mt_m(const MatmulMultiParams &p, hipStream_t s) {
-    switch (mt_of(p.M)) {
-        case 2: return launch_mt_t<T, 2>(p, s);
-        case 4: return launch_mt_t<T, 4>(p, s);
-        default: return launch_mt_t<T, 8>(p, s);
-    }
-}
-
+// Two tokens per launch.
 hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_mt_m<Q4K>(p, s);
-        case kQ5_K: return launch_mt_m<Q5K>(p, s);
-        case kQ6_K: return launch_mt_m<Q6K>(p, s);
-        case kQ8_0: return launch_mt_m<Q80>(p, s);
-        case kIQ4_XS: return launch_mt_m<IQ4XS>(p, s);
+        case kQ4_K: return launch_mt_t<Q4K, 2>(p, s);
+        case kQ5_K: return launch_mt_t<Q5K, 2>(p, s);
+        case kQ6_K: return launch_mt_t<Q6K, 2>(p, s);
+        case kQ8_0: return launch_mt_t<Q80, 2>(p, s);
+        case kIQ4_XS: return launch_mt_t<IQ4XS, 2>(p, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,31 +1,46 @@
 // m27q_mma.hip -- small-M products Y[M][N] = X[M][K] W[N][K]^T on int8 MFMA.
 //
-// For 2 <= M the per-lane dot4 path costs M times the M = 1 work and turns
-// compute-bound at once; here every 32-weight group of 16 weight rows and up
-// to 16 activation rows (tokens) is one v_mfma_i32_16x16x32_i8, which gives
-// the exact integer group sums for all token x row pairs.  The scales are
-// applied in fp32 afterwards: per group j, row r, token t
+// Every 32-weight group of a 16-row set and up to 16 tokens is one
+// v_mfma_i32_16x16x32_i8, which gives the exact integer group sums for all
+// token x row pairs; the scales are applied in fp32 afterwards, per group j,
+// row r, token t:
 //   Q4_K: d_r sc_rj dx_tj S_trj - dmin_r m_rj dx_tj sum(codes_tj)
-//   Q6_K: d_r dx_tj (sc_r,2j (S0 - 32 lo16_tj) + sc_r,2j+1 (S1 - 32 hi16_tj)),
-//         one MFMA per 16-value sub-block (the other half of the operand zero)
-//   Q8_0: d_r dx_tj S_trj
+//   Q6_K: d_r dx_tj (sc_r,2j S0_trj + sc_r,2j+1 S1_trj), the two 16-value
+//         sub-blocks summed apart
+//   Q8_0: d_rj dx_tj S_trj,   IQ4_XS: d_r (ls_rj - 32) dx_tj S_trj
 // which are the per-group terms of the M = 1 products.
 //
-// Lane roles (v_mfma_i32_16x16x32_i8, layout checked on the device):
-//   A (activations): lane l holds token l % 16, K positions 8 q .. 8 q + 7 of
-//                    the group, q = l / 16;
-//   B (weights):     lane l holds row l % 16 of a 16-row tile, same positions;
-//   C:               lane l holds tokens 4 q .. 4 q + 3 of row l % 16.
-// Weights are read straight from the TILED layout (a 16-row tile is two 8-row
-// tiles), the token codes from the quantized activation buffer (L1/L2 hits:
-// every wave at the same K reads the same bytes), the activation scales from
-// LDS, staged transposed ([group][16 tokens]) so a lane reads its 4 tokens at
-// once.  K is split over the KS waves of a workgroup (as in the M = 1 GEMV);
-// each wave covers RT 16-row tiles, and the KS partials are reduced in LDS in a
-// fixed order.  Tokens beyond 16 are handled by further launches.
+// Row packing.  The 16 x 16 output tile is 16 rows x 16 tokens, or, with the
+// packing factor PK = 2, 32 rows x 8 tokens: the K positions of one MFMA are
+// split between two row sets (lane quarters 0-1 hold rows 0-15, quarters 2-3
+// rows 16-31), and the activation operand of a token column is zero in the
+// quarters of the other row set.  Two MFMAs chained through the accumulator
+// then cover the group for both sets.  The integer work is the same, but no
+// lane spends scale arithmetic on padding tokens when M <= 8.
+//
+// Lane roles (v_mfma_i32_16x16x32_i8, layout checked on the device), with
+// quarter q = lane / 16, column c = lane % 16, NQ = 4 / PK quarters per row
+// set, set s = q / NQ, piece lane r = q % NQ:
+//   B (weights):     lane holds row c + 16 s, the 8 positions 8 r + (32/PK) m
+//                    of the group for MFMA m;
+//   A (activations): lane holds token c % (16/PK) at the same positions, or
+//                    zeros if c / (16/PK) != s;
+//   C:               lane holds tokens 4 r .. 4 r + 3 of row c + 16 s.
+// With PK = 2 each MFMA m covers positions 16 m .. 16 m + 15, which keeps
+// the two Q6_K sub-blocks apart.
+//
+// Weights are read from the TILED layout half a unit (four groups) at a time,
+// double buffered; activation codes come from the quantized activation buffer
+// (L1/L2 hits: every wave at the same K reads the same bytes), zero operand
+// lanes from a table of zeros; activation scales are staged in LDS,
+// transposed to [group][token] so a lane reads its 4 tokens at once.  K is
+// split over the KS waves of a workgroup, one row set per workgroup, and the
+// KS partials are added in LDS in a fixed order.  Padding tokens (past M) read
+// a real token's codes; their scales are zero and their outputs are dropped.
 //
 // No reference counterpart: the reference runs prefill and decode one token at
 // a time (src/mono27b_chat.cpp:399-403).
+#include <algorithm>
 #include <type_traits>
 
 #include "m27q_internal.h"
@@ -35,521 +50,671 @@ namespace m27q {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-constexpr int kMmaTok = 16;  // tokens per MFMA (padded with zeros)
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // staging registers (promoted; HIP's uint4 arrays are not)
+
+// Operand bytes of padding lanes: every offset a zero lane reads within one
+// unit (< 264 bytes) lands here.
+__device__ __align__(16) int8_t kMmZero[512] = {};
+
+template <int PK>
+struct Pack {
+    static constexpr int NQ = 4 / PK;   // lane quarters per row set
+    static constexpr int TK = 16 / PK;  // tokens per launch
+    static constexpr int W8 = 32 / PK;  // position stride between a lane's pieces
+    static_assert(PK == 1 || PK == 2, "row packing factor");
+};
 
 __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
-
+__device__ __forceinline__ long as_long(uint2 v) { return as_long(v.x, v.y); }
 __device__ __forceinline__ v4i mfma32(long a, long b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-
-// Activation scales in LDS, transposed to [group][16 tokens]: a lane reads the
-// dx of its 4 tokens (4 q .. 4 q + 3) with one 16-byte read.
-struct ScaleLds {
-    const float *dT;     // [groups][16 tokens]
-    const float *aT;     // [groups][16 tokens], the type's per-group token term (Q4_K only)
-    __device__ float4 dx(int g, int q) const { return *(const float4 *)(dT + g * 16 + 4 * q); }
-    __device__ float aux(int g, int tok) const { return aT[g * 16 + tok]; }
-};
-
+__device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; }
 __device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
 __device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
 __device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
-__device__ __forceinline__ uint32_t u4(const uint4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+// byte e (compile-time) of w as a float: v_cvt_f32_ubyte{0..3}
+__device__ __forceinline__ float ubyte_f(uint32_t w, int e) { return (float)((w >> (8 * e)) & 0xffu); }
+
+// Per-lane geometry.
+template <int PK>
+struct Lane {
+    int q, c, s, r;
+    __device__ explicit Lane(int lane) : q(lane >> 4), c(lane & 15), s(q / Pack<PK>::NQ), r(q % Pack<PK>::NQ) {}
+};
+
+// Activation scales in LDS, [group][TK tokens]; for Q4_K the min term's token
+// factor in the same shape.
+template <int PK>
+struct ScaleLds {
+    const float *dT, *aT;
+    __device__ float4 dx(int g, int r) const { return *(const float4 *)(dT + g * Pack<PK>::TK + 4 * r); }
+};
+
+// Activation operands of one half unit: a[group][piece].
+template <int PK>
+struct AFrag {
+    uint2 a[4][PK];
+};
+
+// From the lane's token record in LDS (its piece offset 8 r included).
+template <int PK>
+__device__ __forceinline__ void load_act(AFrag<PK> &f, const uint8_t *ar, int st) {
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg)
+#pragma unroll
+        for (int m = 0; m < PK; ++m) f.a[jg][m] = ld8(ar + 32 * (4 * st + jg) + Pack<PK>::W8 * m);
+}
 
 // ------------------------------------------------------------ Q4_K, Q5_K --
 // Q5_K is Q4_K with a fifth code bit per weight: bit j of qh[l] for position l
 // of group j (exec:953-969), added to the operand bytes as 16.
 template <bool Q5>
-struct MmaQ4KT {
-    static constexpr int kGroups = 8;  // 32-weight groups per unit
+struct MmQ4KT {
+    static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
     // The min term's token factor: dx * (sum of the 32 codes).
     __device__ static float stage_aux(float d, uint32_t s) { return d * (float)(s_lo(s) + s_hi(s)); }
+    template <int PK>
     struct Frag {
-        uint2 qs[4];  // bytes 32 g + 8 q .. +8 of the row's quants, g = 0..3
-        uint4 h;      // d | dmin, scales[12]
-        uint2 qh;     // Q5_K: qh bytes 8 q .. +8
+        uint2 qs[2][PK];  // the two 32-byte qs chunks of the half unit
+        uint4 h;          // d | dmin, scales[12]
+        uint2 qh[Q5 ? PK : 1];
     };
-    // unit: start of the 8-row TILED unit holding row i
-    __device__ static Frag load(const uint8_t *unit, int i, int q) {
-        Frag f;
-        const uint8_t *qs = unit + 128 + 128 * i + 8 * q;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) f.qs[g] = *(const uint2 *)(qs + 32 * g);
-        f.h = *(const uint4 *)(unit + 16 * i);
-        if constexpr (Q5) f.qh = *(const uint2 *)(unit + kQ5KTQh + 32 * i + 8 * q);
-        return f;
+    // LDS row record: header 16 | qs 128 (| Q5_K qh 32).  Chunk c (16 bytes)
+    // of the TILED unit of 8-row tile t goes to:
+    static constexpr int kRowBytes = Q5 ? 176 : 144;
+    __device__ static int lds_dst(int t, int c, int) {
+        if (c < 8) return (8 * t + c) * kRowBytes;
+        if (c < 72) return (8 * t + ((c - 8) >> 3)) * kRowBytes + 16 + 16 * ((c - 8) & 7);
+        return (8 * t + ((c - 72) >> 1)) * kRowBytes + 144 + 16 * ((c - 72) & 1);  // Q5_K qh
     }
-    __device__ static long operand(const Frag &f, int j) {
-        const uint2 w = f.qs[j >> 1];
-        const int sh = 4 * (j & 1);
+    template <int PK>
+    __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int) {
+        constexpr int W8 = Pack<PK>::W8;
+        const uint8_t *rb = wl + row * kRowBytes;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int m = 0; m < PK; ++m) f.qs[cc][m] = ld8(rb + 16 + 64 * st + 32 * cc + 8 * r + W8 * m);
+        f.h = *(const uint4 *)rb;
+        if constexpr (Q5) {
+#pragma unroll
+            for (int m = 0; m < PK; ++m) f.qh[m] = ld8(rb + 144 + 8 * r + W8 * m);
+        }
+    }
+    template <int PK, int ST>
+    __device__ static long operand(const Frag<PK> &f, int jg, int m) {
+        const uint2 w = f.qs[jg >> 1][m];
+        const int sh = 4 * (jg & 1);
         uint32_t lo = (w.x >> sh) & 0x0f0f0f0fu, hi = (w.y >> sh) & 0x0f0f0f0fu;
         if constexpr (Q5) {
-            lo |= ((f.qh.x >> j) & 0x01010101u) << 4;
-            hi |= ((f.qh.y >> j) & 0x01010101u) << 4;
+            const int g = 4 * ST + jg;
+            lo |= ((f.qh[m].x >> g) & 0x01010101u) << 4;
+            hi |= ((f.qh[m].y >> g) & 0x01010101u) << 4;
         }
         return as_long(lo, hi);
     }
-    // Main term: acc[t][e] += d sc_j * dx_j,e * S_j,e per group (VALU, the
-    // group's integer sums from the MFMA).  Min term: cm[t] += sum_j aux_j,tok *
-    // (dmin m_j,row), an fp32 MFMA over the unit's 8 groups (2 x K = 4).
-    template <int RT>
-    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
-                                      int q, int r16, float (&acc)[RT][4], v4f (&cm)[RT]) {
-        uint32_t scA[RT], scB[RT];
-        float d[RT];
+    template <int PK, int ST>
+    __device__ static void mma(const Frag<PK> &f, const AFrag<PK> &a, int jg, const Lane<PK> &, v4i &S, v4i &) {
+        S = mfma32(as_long(a.a[jg][0]), operand<PK, ST>(f, jg, 0), v4i{0, 0, 0, 0});
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            // get_scale_min_k4 (exec:690-693) for all 8 pairs at once, one byte each
-            const uint4 h = f[t].h;
-            scA[t] = h.y & 0x3f3f3f3fu;
-            scB[t] = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-            const uint32_t m03 = h.z & 0x3f3f3f3fu;
-            const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-            d[t] = f16_bits_to_f32(h.x);
-            const float dmin = f16_bits_to_f32(h.x >> 16);
-            const float b0 = dmin * (float)((m03 >> (8 * q)) & 0xffu);
-            const float b1 = dmin * (float)((m47 >> (8 * q)) & 0xffu);
-            cm[t] = mfma_f32(sl.aux(g0 + q, r16), b0, cm[t]);
-            cm[t] = mfma_f32(sl.aux(g0 + 4 + q, r16), b1, cm[t]);
-        }
-        // Software pipeline: the MFMAs of group j + 1 are issued before the
-        // scale arithmetic of group j; the scheduling barrier keeps each group's
-        // values local.
-        // The activation scales of group j + 1 are read from LDS one group
-        // ahead as well, so no group waits on its own LDS read.
-        v4i c[RT];
-#pragma unroll
-        for (int t = 0; t < RT; ++t) c[t] = mfma32(a[0], operand(f[t], 0), v4i{0, 0, 0, 0});
-        float4 dx = sl.dx(g0, q);
-#pragma unroll
-        for (int j = 0; j < kGroups; ++j) {
-            v4i cn[RT];
-#pragma unroll
-            for (int t = 0; t < RT; ++t) cn[t] = j + 1 < kGroups ? mfma32(a[j + 1], operand(f[t], j + 1), v4i{0, 0, 0, 0}) : c[t];
-            const float4 dxn = j + 1 < kGroups ? sl.dx(g0 + j + 1, q) : dx;
-#pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const uint32_t scw = j < 4 ? scA[t] : scB[t];
-                const float ws = d[t] * (float)((scw >> (8 * (j & 3))) & 0xffu);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(ws, f4(dx, e) * (float)c[t][e], acc[t][e]);
-                c[t] = cn[t];
-            }
-            dx = dxn;
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int m = 1; m < PK; ++m) S = mfma32(as_long(a.a[jg][m]), operand<PK, ST>(f, jg, m), S);
     }
+    // Per half unit: main-term group scales and the min term (an fp32 MFMA,
+    // K = 4: NQ groups of each row set per MFMA).
+    template <int PK, int ST>
+    struct Half {
+        float d;
+        uint32_t scw;
+        __device__ Half(const Frag<PK> &f, const ScaleLds<PK> &sl, int gu, const Lane<PK> &L, bool areal, int atok,
+                        v4f &cm) {
+            const uint4 h = f.h;
+            d = f16_bits_to_f32(h.x);
+            const float dmin = f16_bits_to_f32(h.x >> 16);
+            // get_scale_min_k4 (exec:690-693) for the four groups of this half,
+            // one byte each
+            scw = ST == 0 ? (h.y & 0x3f3f3f3fu) : ((h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u));
+            const uint32_t mw = ST == 0 ? (h.z & 0x3f3f3f3fu) : (((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u));
+            constexpr int NQ = Pack<PK>::NQ, TK = Pack<PK>::TK;
+#pragma unroll
+            for (int n = 0; n < PK; ++n) {
+                const int gl = NQ * n + L.r;  // group within the half, this lane's K index
+                const float bm = dmin * (float)((mw >> (8 * gl)) & 0xffu);
+                const float av = sl.aT[(gu + 4 * ST + gl) * TK + atok];
+                cm = mfma_f32(areal ? av : 0.f, bm, cm);
+            }
+        }
+        __device__ void scale(int jg, const float4 &dx, const v4i &S, const v4i &, float (&acc)[4], float (&)[4]) const {
+            const float ws = d * ubyte_f(scw, jg);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(ws, f4(dx, e) * (float)S[e], acc[e]);
+        }
+        __device__ void finish(float (&)[4], float (&)[4]) const {}
+    };
 };
 
-using MmaQ4K = MmaQ4KT<false>;
-using MmaQ5K = MmaQ4KT<true>;
+using MmQ4K = MmQ4KT<false>;
+using MmQ5K = MmQ4KT<true>;
 
 // ------------------------------------------------------------------ Q6_K --
-struct MmaQ6K {
-    static constexpr int kGroups = 8;
+struct MmQ6K {
+    static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = kQ6KUnit;
     static constexpr bool kAux = false;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
+    template <int PK>
     struct Frag {
-        uint2 ql[2][2];  // [half h][r & 1]: ql bytes 64 h + 32 (r & 1) + 8 q .. +8
-        uint2 qh[2];     // [half h]: qh bytes 32 h + 8 q .. +8
-        uint4 sc;        // 16 int8 scales
-        uint32_t d;      // f16 bits
+        uint2 ql[2][PK];  // [rr & 1][piece]: ql bytes 64 h + 32 (rr & 1) + ...
+        uint2 qh[PK];     // qh bytes 32 h + ...
+        uint2 sc;         // the half's 8 int8 scales
+        uint32_t d;       // f16 bits
     };
-    __device__ static Frag load(const uint8_t *unit, int i, int q) {
-        Frag f;
-        const uint8_t *ql = unit + kQ6KTQl + 128 * i + 8 * q;
-        const uint8_t *qh = unit + kQ6KTQh + 64 * i + 8 * q;
+    // LDS row record: ql 128 | qh 64 | scales 16 | pad 32; the eight d of a
+    // tile in the side area (16 bytes per tile).
+    static constexpr int kRowBytes = 240;
+    __device__ static int lds_dst(int t, int c, int side) {
+        if (c < 64) return (8 * t + (c >> 3)) * kRowBytes + 16 * (c & 7);
+        if (c < 96) return (8 * t + ((c - 64) >> 2)) * kRowBytes + 128 + 16 * ((c - 64) & 3);
+        if (c < 104) return (8 * t + (c - 96)) * kRowBytes + 192;
+        return side + 16 * t;
+    }
+    template <int PK>
+    __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int side) {
+        constexpr int W8 = Pack<PK>::W8;
+        const uint8_t *rb = wl + row * kRowBytes;
+        const uint8_t *ql = rb + 64 * st + 8 * r;
+        const uint8_t *qh = rb + 128 + 32 * st + 8 * r;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            f.ql[h][0] = *(const uint2 *)(ql + 64 * h);
-            f.ql[h][1] = *(const uint2 *)(ql + 64 * h + 32);
-            f.qh[h] = *(const uint2 *)(qh + 32 * h);
+        for (int m = 0; m < PK; ++m) {
+            f.ql[0][m] = ld8(ql + W8 * m);
+            f.ql[1][m] = ld8(ql + 32 + W8 * m);
+            f.qh[m] = ld8(qh + W8 * m);
         }
-        f.sc = *(const uint4 *)(unit + kQ6KTSc + 16 * i);
-        f.d = *(const uint16_t *)(unit + kQ6KTD + 2 * i);
-        return f;
+        f.sc = ld8(rb + 192 + 8 * st);
+        f.d = *(const uint16_t *)(wl + side + 16 * (row >> 3) + 2 * (row & 7));
     }
-    __device__ static int sc_byte(const uint4 &sc, int k) {
-        return (int)(int8_t)(u4(sc, k >> 2) >> (8 * (k & 3)));
-    }
-    // Group j = 4 h + r covers K 32 j .. 32 j + 31 of the block (half h, quarter r
-    // of the q6k_val index map, exec:1026-1048); sub-block 2 j (scale 8 h + 2 r)
-    // is held by lane quarters 0, 1 and sub-block 2 j + 1 by quarters 2, 3.
-    // The 6-bit codes b become the signed q = b - 32 per byte:
+    // Group rr of half h covers block positions 128 h + 32 rr .. + 31 (the
+    // q6k_val index map, exec:1026-1048): low 4 bits from the ql bytes of
+    // quarter rr & 1 (high nibbles for rr >= 2), high 2 bits at bit 2 rr of
+    // the qh bytes.  The 6-bit codes b become the signed q = b - 32 per byte:
     // (b + 0x60) ^ 0x80 = b - 32 (mod 256) for 0 <= b <= 63, with no carry
     // between bytes.
-    __device__ static long operand(const Frag &f, int j) {
-        const int h = j >> 2, r = j & 3;
-        const uint2 l = f.ql[h][r & 1], hb = f.qh[h];
-        const int nsh = 4 * (r >> 1), hsh = 2 * r;
+    template <int PK>
+    __device__ static long operand(const Frag<PK> &f, int rr, int m) {
+        const uint2 l = f.ql[rr & 1][m], hb = f.qh[m];
+        const int nsh = 4 * (rr >> 1), hsh = 2 * rr;
         const uint32_t b0 = ((l.x >> nsh) & 0x0f0f0f0fu) + (((hb.x >> hsh) & 0x03030303u) << 4) + 0x60606060u;
         const uint32_t b1 = ((l.y >> nsh) & 0x0f0f0f0fu) + (((hb.y >> hsh) & 0x03030303u) << 4) + 0x60606060u;
         return as_long(b0 ^ 0x80808080u, b1 ^ 0x80808080u);
     }
-    // acc[t][e] += d * sum_j dx_j,e (sc_2j S0_j,e + sc_2j+1 S1_j,e); the group
-    // sums are exact integers, d is applied once per unit.
-    template <int RT>
-    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
-                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
-        const bool lo_quarter = q < 2;
-        float u[RT][4];
-#pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) u[t][e] = 0.f;
-        // Two MFMAs per group, one per 16-value sub-block (the lane quarters
-        // holding the other sub-block pass zeros); pipelined as for Q4_K.
-        v4i c0[RT], c1[RT];
-        auto mm = [&](int j, v4i (&x0)[RT], v4i (&x1)[RT]) {
-#pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const long b = operand(f[t], j);
-                x0[t] = mfma32(a[j], lo_quarter ? b : 0l, v4i{0, 0, 0, 0});
-                x1[t] = mfma32(a[j], lo_quarter ? 0l : b, v4i{0, 0, 0, 0});
-            }
-        };
-        mm(0, c0, c1);
-        float4 dx = sl.dx(g0, q);  // one group ahead, as for Q4_K
-#pragma unroll
-        for (int j = 0; j < kGroups; ++j) {
-            v4i n0[RT], n1[RT];
-            if (j + 1 < kGroups) mm(j + 1, n0, n1);
-            const int h = j >> 2, r = j & 3;
-            const float4 dxn = j + 1 < kGroups ? sl.dx(g0 + j + 1, q) : dx;
-#pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const int s0 = sc_byte(f[t].sc, 8 * h + 2 * r), s1 = sc_byte(f[t].sc, 8 * h + 2 * r + 1);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int v = __mul24(s0, c0[t][e]) + __mul24(s1, c1[t][e]);
-                    u[t][e] = fmaf(f4(dx, e), (float)v, u[t][e]);
-                }
-                if (j + 1 < kGroups) {
-                    c0[t] = n0[t];
-                    c1[t] = n1[t];
-                }
-            }
-            dx = dxn;
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const float d = f16_bits_to_f32(f[t].d);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(d, u[t][e], acc[t][e]);
+    // S0 / S1: the sums over the two 16-value sub-blocks.  PK = 1: quarters
+    // 0-1 hold sub-block 0, so two MFMAs with the other half of the weight
+    // operand zero; PK = 2: MFMA m covers sub-block m.
+    template <int PK, int ST>
+    __device__ static void mma(const Frag<PK> &f, const AFrag<PK> &a, int jg, const Lane<PK> &L, v4i &S0, v4i &S1) {
+        if constexpr (PK == 1) {
+            const long b = operand<PK>(f, jg, 0);
+            const bool lo = L.q < 2;
+            S0 = mfma32(as_long(a.a[jg][0]), lo ? b : 0l, v4i{0, 0, 0, 0});
+            S1 = mfma32(as_long(a.a[jg][0]), lo ? 0l : b, v4i{0, 0, 0, 0});
+        } else {
+            S0 = mfma32(as_long(a.a[jg][0]), operand<PK>(f, jg, 0), v4i{0, 0, 0, 0});
+            S1 = mfma32(as_long(a.a[jg][1]), operand<PK>(f, jg, 1), v4i{0, 0, 0, 0});
         }
     }
+    template <int PK, int ST>
+    struct Half {
+        uint2 sc;
+        float d;
+        __device__ Half(const Frag<PK> &f, const ScaleLds<PK> &, int, const Lane<PK> &, bool, int, v4f &)
+            : sc(f.sc), d(f16_bits_to_f32(f.d)) {}
+        // u += dx * (sc_2j S0 + sc_2j+1 S1): exact integers until the dx
+        // product; d is applied once per unit.
+        __device__ void scale(int rr, const float4 &dx, const v4i &S0, const v4i &S1, float (&)[4],
+                              float (&u)[4]) const {
+            const uint32_t w = rr < 2 ? sc.x : sc.y;
+            const int s0 = (int)(int8_t)(w >> (16 * (rr & 1))), s1 = (int)(int8_t)(w >> (16 * (rr & 1) + 8));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int v = __mul24(s0, S0[e]) + __mul24(s1, S1[e]);
+                u[e] = fmaf(f4(dx, e), (float)v, u[e]);
+            }
+        }
+        __device__ void finish(float (&acc)[4], float (&u)[4]) const {
+            if constexpr (ST == 1) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[e] = fmaf(d, u[e], acc[e]);
+                    u[e] = 0.f;
+                }
+            }
+        }
+    };
 };
 
 // ------------------------------------------------------------------ Q8_0 --
-struct MmaQ80 {
-    static constexpr int kGroups = 4;  // blocks of 32 per TILED unit
+struct MmQ80 {
+    static constexpr int kGroups = 4, kSteps = 1;  // four 32-blocks per TILED unit
     static constexpr int kUnitBytes = kQ80Unit;
     static constexpr bool kAux = false;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
+    template <int PK>
     struct Frag {
-        uint2 qs[4];
+        uint2 qs[4][PK];
         uint2 d;  // 4 f16 scales
     };
-    __device__ static Frag load(const uint8_t *unit, int i, int q) {
-        Frag f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) f.qs[k] = *(const uint2 *)(unit + 128 * i + 32 * k + 8 * q);
-        f.d = *(const uint2 *)(unit + kQ80TD + 8 * i);
-        return f;
+    // LDS row record: qs 128 | pad 16; the rows' d (8 bytes each) in the side
+    // area, 64 bytes per tile.
+    static constexpr int kRowBytes = 144;
+    __device__ static int lds_dst(int t, int c, int side) {
+        if (c < 64) return (8 * t + (c >> 3)) * kRowBytes + 16 * (c & 7);
+        return side + 64 * t + 16 * (c - 64);
     }
-    template <int RT>
-    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
-                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
+    template <int PK>
+    __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int, int side) {
+        const uint8_t *rb = wl + row * kRowBytes;
 #pragma unroll
-        for (int j = 0; j < kGroups; ++j) {
-            const float4 dx = sl.dx(g0 + j, q);
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const v4i c = mfma32(a[j], as_long(f[t].qs[j].x, f[t].qs[j].y), v4i{0, 0, 0, 0});
-                const uint32_t dw2 = j < 2 ? f[t].d.x : f[t].d.y;
-                const float dw = f16_bits_to_f32(dw2 >> (16 * (j & 1)));
+            for (int m = 0; m < PK; ++m) f.qs[k][m] = ld8(rb + 32 * k + 8 * r + Pack<PK>::W8 * m);
+        f.d = ld8(wl + side + 64 * (row >> 3) + 8 * (row & 7));
+    }
+    template <int PK, int ST>
+    __device__ static void mma(const Frag<PK> &f, const AFrag<PK> &a, int jg, const Lane<PK> &, v4i &S, v4i &) {
+        S = mfma32(as_long(a.a[jg][0]), as_long(f.qs[jg][0]), v4i{0, 0, 0, 0});
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(dw * f4(dx, e), (float)c[e], acc[t][e]);
-            }
+        for (int m = 1; m < PK; ++m) S = mfma32(as_long(a.a[jg][m]), as_long(f.qs[jg][m]), S);
+    }
+    template <int PK, int ST>
+    struct Half {
+        uint2 dw;
+        __device__ Half(const Frag<PK> &f, const ScaleLds<PK> &, int, const Lane<PK> &, bool, int, v4f &) : dw(f.d) {}
+        __device__ void scale(int k, const float4 &dx, const v4i &S, const v4i &, float (&acc)[4], float (&)[4]) const {
+            const float d = f16_bits_to_f32((k < 2 ? dw.x : dw.y) >> (16 * (k & 1)));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(d * f4(dx, e), (float)S[e], acc[e]);
         }
-    }
+        __device__ void finish(float (&)[4], float (&)[4]) const {}
+    };
 };
 
 // ---------------------------------------------------------------- IQ4_XS --
-// Group j of the block: lane quarter q holds positions 8 q .. 8 q + 7, the low
-// nibbles of qs bytes 16 j + 8 q (q < 2) or the high nibbles of 16 j + 8 (q - 2)
-// (q >= 2), through the 16-entry table; scale d (ls_j - 32) per group.
-struct MmaIQ4XS {
-    static constexpr int kGroups = 8;
+// Group j's 16 qs bytes hold positions l (low nibble) and l + 16 (high
+// nibble) of byte l.  A lane's 8-position piece is the low or high nibbles of
+// 8 consecutive bytes: PK = 1, quarter q: bytes 8 (q & 1), nibble q >> 1;
+// PK = 2, piece m: bytes 8 r, nibble m.  Codes go through the 16-entry table;
+// scale d (ls_j - 32) per group.
+struct MmIQ4XS {
+    static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = kIQ4XSUnit;
     static constexpr bool kAux = false;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
+    template <int PK>
     struct Frag {
-        uint2 qs[8];  // 8 qs bytes of each group
-        uint2 hd;     // d | scales_h << 16, scales_l[4]
+        uint2 qs[4];
+        uint2 hd;  // d | scales_h << 16, scales_l[4]
+        int nib;   // PK = 1: the lane's nibble
     };
-    __device__ static Frag load(const uint8_t *unit, int i, int q) {
-        Frag f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) f.qs[j] = *(const uint2 *)(unit + 128 * i + 16 * j + 8 * (q & 1));
-        f.hd = *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i);
-        return f;
+    // LDS row record: qs 128 | pad 16; the rows' headers (8 bytes each) in
+    // the side area, 64 bytes per tile.
+    static constexpr int kRowBytes = 144;
+    __device__ static int lds_dst(int t, int c, int side) {
+        if (c < 64) return (8 * t + (c >> 3)) * kRowBytes + 16 * (c & 7);
+        return side + 64 * t + 16 * (c - 64);
     }
-    template <int RT>
-    __device__ static void accumulate(const Frag (&f)[RT], const long (&a)[kGroups], const ScaleLds &sl, int g0,
-                                      int q, int, float (&acc)[RT][4], v4f (&)[RT]) {
-        const int nsh = q < 2 ? 0 : 4;
+    template <int PK>
+    __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int side) {
+        // PK = 1: r = q; bytes 8 (q & 1); PK = 2: bytes 8 r
+        const int boff = PK == 1 ? 8 * (r & 1) : 8 * r;
+        const uint8_t *rb = wl + row * kRowBytes;
 #pragma unroll
-        for (int j = 0; j < kGroups; ++j) {
-            const float4 dx = sl.dx(g0 + j, q);
+        for (int jg = 0; jg < 4; ++jg) f.qs[jg] = ld8(rb + 16 * (4 * st + jg) + boff);
+        f.hd = ld8(wl + side + 64 * (row >> 3) + 8 * (row & 7));
+        f.nib = PK == 1 ? 4 * (r >> 1) : 0;
+    }
+    template <int PK>
+    __device__ static long operand(const Frag<PK> &f, int jg, int m) {
+        const int sh = PK == 1 ? f.nib : 4 * m;
+        const uint2 w = f.qs[jg];
+        return as_long(iq4_lut((w.x >> sh) & 0x0f0f0f0fu), iq4_lut((w.y >> sh) & 0x0f0f0f0fu));
+    }
+    template <int PK, int ST>
+    __device__ static void mma(const Frag<PK> &f, const AFrag<PK> &a, int jg, const Lane<PK> &, v4i &S, v4i &) {
+        S = mfma32(as_long(a.a[jg][0]), operand<PK>(f, jg, 0), v4i{0, 0, 0, 0});
 #pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const uint2 w = f[t].qs[j];
-                const long b = as_long(iq4_lut((w.x >> nsh) & 0x0f0f0f0fu), iq4_lut((w.y >> nsh) & 0x0f0f0f0fu));
-                const v4i c = mfma32(a[j], b, v4i{0, 0, 0, 0});
-                const int ls = (int)(((f[t].hd.y >> (8 * (j >> 1) + 4 * (j & 1))) & 15u) |
-                                     (((f[t].hd.x >> (16 + 2 * j)) & 3u) << 4)) - 32;
-                const float dl = f16_bits_to_f32(f[t].hd.x) * (float)ls;
+        for (int m = 1; m < PK; ++m) S = mfma32(as_long(a.a[jg][m]), operand<PK>(f, jg, m), S);
+    }
+    template <int PK, int ST>
+    struct Half {
+        uint2 hd;
+        __device__ Half(const Frag<PK> &f, const ScaleLds<PK> &, int, const Lane<PK> &, bool, int, v4f &) : hd(f.hd) {}
+        __device__ void scale(int jg, const float4 &dx, const v4i &S, const v4i &, float (&acc)[4], float (&)[4]) const {
+            const int j = 4 * ST + jg;
+            const int ls = (int)(((hd.y >> (8 * (j >> 1) + 4 * (j & 1))) & 15u) | (((hd.x >> (16 + 2 * j)) & 3u) << 4)) - 32;
+            const float dl = f16_bits_to_f32(hd.x) * (float)ls;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(dl * f4(dx, e), (float)c[e], acc[t][e]);
-            }
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dl * f4(dx, e), (float)S[e], acc[e]);
         }
+        __device__ void finish(float (&)[4], float (&)[4]) const {}
+    };
+};
+
+template <int V>
+struct IntTag {
+    static constexpr int value = V;
+};
+
+// One half unit: the four groups' MFMAs, each issued one group ahead of the
+// previous group's scale arithmetic.
+template <class T, int PK, int ST>
+__device__ __forceinline__ void compute_half(const typename T::template Frag<PK> &f, const AFrag<PK> &a,
+                                             const ScaleLds<PK> &sl, int gu, const Lane<PK> &L, bool areal, int atok,
+                                             float (&acc)[4], float (&u)[4], v4f &cm) {
+    const typename T::template Half<PK, ST> hs(f, sl, gu, L, areal, atok, cm);
+    v4i S0, S1;
+    T::template mma<PK, ST>(f, a, 0, L, S0, S1);
+    float4 dx = sl.dx(gu + 4 * ST, L.r);
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+        v4i N0, N1;
+        float4 dxn = dx;
+        if (jg + 1 < 4) {
+            T::template mma<PK, ST>(f, a, jg + 1, L, N0, N1);
+            dxn = sl.dx(gu + 4 * ST + jg + 1, L.r);
+        }
+        hs.scale(jg, dx, S0, S1, acc, u);
+        if (jg + 1 < 4) {
+            S0 = N0;
+            S1 = N1;
+        }
+        dx = dxn;
+        __builtin_amdgcn_sched_barrier(0);
     }
+    hs.finish(acc, u);
+}
+
+// Per-wave LDS staging area for one unit (bytes):
+//   W: 16 PK row records of T::kRowBytes, then a side area (64 bytes per tile)
+//   A: TK token records of 32 G + 16 bytes (G groups of codes + pad), then,
+//      for PK = 2, one record of zeros for the operand lanes of the other set
+//   S: dT [G][TK] and, for Q4_K, aT [G][TK] floats
+//   a 16-byte slot that absorbs the writes of lanes past the data
+// The paddings keep the MFMA-layout reads free of bank conflicts: the row
+// strides 144, 176, 240 and the token strides 272, 144 put the 16 rows (or
+// tokens) of a half wave on distinct 4-bank groups.
+template <class T, int PK>
+struct Stage {
+    static constexpr int G = T::kGroups, TK = Pack<PK>::TK, UE = 32 * G, UB = T::kUnitBytes;
+    static constexpr int kSide = 16 * PK * T::kRowBytes;
+    static constexpr int kW = kSide + 2 * PK * 64;
+    static constexpr int kARow = UE + 16;
+    static constexpr int oA = kW;
+    static constexpr int oZero = oA + TK * kARow;
+    static constexpr int oS = oZero + (PK == 2 ? UE : 0);
+    static constexpr int oDummy = oS + G * TK * 4 * (T::kAux ? 2 : 1);
+    static constexpr int kBytes = (oDummy + 16 + 15) / 16 * 16;
+    static constexpr int kWChunks = 2 * PK * UB / 16;  // 16-byte chunks of the set's unit
+    static constexpr int kNW = (kWChunks + kWave - 1) / kWave;
+    static constexpr int kAChunks = TK * UE / 16;
+    static constexpr int kNA = (kAChunks + kWave - 1) / kWave;
+    static constexpr int kSLanes = TK * G / 4;  // lanes staging 4 scales each
+    static_assert(kSLanes <= kWave, "scale staging lanes");
+    static_assert(kAChunks % kWave == 0, "whole activation staging rounds");
+    static_assert(UB % 16 == 0 && kARow % 16 == 0 && T::kRowBytes % 16 == 0, "16-byte staging");
 };
 
-// One unit (a K range of kGroups x 32) of activation operands.
-template <class T>
-struct ActUnit {
-    long a[T::kGroups];
-};
-
-// KS waves split K; each wave covers RT 16-row tiles.  Up to kMaxMulti weights
-// of one K share the launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
-template <class T, int KS, int RT>
-__global__ __launch_bounds__(kWave *KS) void k_matmul_mfma(MatmulMultiParams p, int m0) {
+// One workgroup: one row set of 16 PK rows of one matrix, K split over the KS
+// waves.  Each wave streams its K slice one unit at a time: 16-byte loads of
+// the unit's weight tiles, activation codes and scales into registers (issued
+// while the previous unit computes), written to the wave's LDS area, read
+// back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
+// launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
+template <class T, int PK, int KS>
+__global__ __launch_bounds__(kWave *KS, 3) void k_matmul_mfma(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int G = T::kGroups;
-    constexpr int TR = 16 * RT;  // weight rows per workgroup
-    const int lane = (int)(threadIdx.x & 63), q = lane >> 4, r16 = lane & 15;
+    using SG = Stage<T, PK>;
+    constexpr int G = T::kGroups, NS = T::kSteps, TK = Pack<PK>::TK, UE = SG::UE, UB = SG::UB;
+    constexpr int CPU = UB / 16;  // chunks per tile unit
+    const int lane = (int)(threadIdx.x & 63);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const Lane<PK> L(lane);
     int mi = 0;
 #pragma unroll
     for (int k = 1; k < kMaxMulti; ++k)
         if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) mi = k;
     const uint8_t *Wm = p.W[mi];
     const int rc = p.rc[mi];
-    const int M = min(p.M - m0, kMmaTok);
+    const int Mloc = min(p.M - m0, TK);
     const int ngroups = p.K / 32;
-    const int gpad = p.upr * G;  // groups of whole units (Q8_0 units can pass K)
     const int ntiles8 = (rc + kTileRows - 1) / kTileRows;
-    const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * TR;
+    const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * 16 * PK;
+    uint8_t *wl = smem + (size_t)wave * SG::kBytes;
 
-    // Activation scales, transposed to [group][16 tokens] (zeros past M and K),
-    // and for Q4_K the min term's token factor in the same shape.
-    float *dT = (float *)smem;
-    float *aT = (float *)(smem + (size_t)gpad * kMmaTok * 4);
-    // Loads issued kBatch at a time before any is used: a few L2 round trips
-    // instead of one per entry.
-    constexpr int kBatch = 8;
-    for (int i0 = (int)threadIdx.x; i0 < gpad * kMmaTok; i0 += kBatch * KS * kWave) {
-        float d[kBatch];
-        uint32_t sw[kBatch];
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int idx = i0 + b * KS * kWave;
-            const int g = idx / kMmaTok, t = idx % kMmaTok;
-            const bool in = idx < gpad * kMmaTok && t < M && g < ngroups;
-            const size_t src = in ? (size_t)(m0 + t) * ngroups + g : 0;
-            d[b] = p.xd[src];
-            sw[b] = T::kAux ? p.xs[src] : 0u;
-            if (!in) {
-                d[b] = 0.f;
-                sw[b] = 0u;
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int idx = i0 + b * KS * kWave;
-            if (idx < gpad * kMmaTok) {
-                dT[idx] = d[b];
-                if (T::kAux) aT[idx] = T::stage_aux(d[b], sw[b]);
-            }
-        }
-    }
-    const ScaleLds sl{dT, aT};
-    float *red = (float *)(smem + (size_t)gpad * kMmaTok * (T::kAux ? 8 : 4));  // [KS][16 tokens][TR]
-    __syncthreads();
-
-    // This wave's K slice (units) and the lane's rows.
+    // This wave's K slice (units).
     const int U = p.upr / KS, rem = p.upr % KS;
     const int ub = wave * U + min(wave, rem);
     const int nu = U + (wave < rem ? 1 : 0);
-    const uint8_t *unit0[RT];
-    int irow[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int row = row0 + 16 * t + r16;
-        const int tt = min(row / kTileRows, ntiles8 - 1);  // rows past the end: reread the last tile
-        unit0[t] = Wm + (size_t)tt * p.upr * T::kUnitBytes;
-        irow[t] = row % kTileRows;
-    }
-    const bool tok_in = r16 < M;
-    const int8_t *xrow = p.xq + (size_t)(m0 + (tok_in ? r16 : 0)) * p.K + 8 * q;
 
-    // Unconditional loads and a bit mask (a select on the loaded value would be
-    // turned into a branch around each load, with a wait inside it).
-    const uint32_t tmask = tok_in ? 0xffffffffu : 0u;
-    auto load_act = [&](ActUnit<T> &au, int u) {
+    // Staging map of this lane: weight chunks (tiles past the end reread the
+    // last tile), activation chunks (padding tokens read token m0), scales.
+    size_t goff[SG::kNW];
+    int wdst[SG::kNW];
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const int g = u * G + j;
-            const uint2 v = *(const uint2 *)(xrow + (size_t)min(g, ngroups - 1) * 32);
-            const uint32_t msk = g < ngroups ? tmask : 0u;
-            au.a[j] = as_long(v.x & msk, v.y & msk);
+    for (int n = 0; n < SG::kNW; ++n) {
+        const int id = n * kWave + lane;
+        const bool ok = id < SG::kWChunks;
+        const int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
+        const int tile = min(row0 / kTileRows + t, ntiles8 - 1);
+        goff[n] = (size_t)tile * p.upr * UB + 16 * c;
+        wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
+    }
+    size_t aoff[SG::kNA];
+    int adst[SG::kNA];
+#pragma unroll
+    for (int n = 0; n < SG::kNA; ++n) {
+        const int id = n * kWave + lane;
+        const int tok = id / (UE / 16), c = id % (UE / 16);
+        aoff[n] = (size_t)(m0 + (tok < Mloc ? tok : 0)) * p.K + 16 * c;
+        adst[n] = SG::oA + tok * SG::kARow + 16 * c;
+    }
+    const int s_tok = lane / (G / 4), s_h = lane % (G / 4);
+    const bool s_on = lane < SG::kSLanes;
+    const bool s_tok_in = s_on && s_tok < Mloc;
+    const size_t s_row = (size_t)(m0 + (s_tok_in ? s_tok : 0)) * ngroups;
+
+    v4u rw[SG::kNW], ra[SG::kNA];
+    float sd[4];
+    uint32_t ss[4] = {0u, 0u, 0u, 0u};
+    auto issue = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < SG::kNW; ++n) rw[n] = *(const v4u *)(Wm + (size_t)u * UB + goff[n]);
+#pragma unroll
+        for (int n = 0; n < SG::kNA; ++n) ra[n] = *(const v4u *)(p.xq + (size_t)u * UE + aoff[n]);
+        const int g0 = u * G + 4 * s_h;
+        if constexpr (G == 8) {  // whole units: rows of 8 k groups, 16-byte aligned
+            const float4 d = *(const float4 *)(p.xd + s_row + g0);
+            sd[0] = d.x;
+            sd[1] = d.y;
+            sd[2] = d.z;
+            sd[3] = d.w;
+            if constexpr (T::kAux) {
+                const uint4 v = *(const uint4 *)(p.xs + s_row + g0);
+                ss[0] = v.x;
+                ss[1] = v.y;
+                ss[2] = v.z;
+                ss[3] = v.w;
+            }
+        } else {  // Q8_0: the last unit can pass K
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sd[e] = p.xd[s_row + min(g0 + e, ngroups - 1)];
         }
     };
-    auto load_w = [&](typename T::Frag (&f)[RT], int u) {
+    auto commit = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t) f[t] = T::load(unit0[t] + (size_t)u * T::kUnitBytes, irow[t], q);
+        for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+#pragma unroll
+        for (int n = 0; n < SG::kNA; ++n) *(v4u *)(wl + adst[n]) = ra[n];
+        float *dT = (float *)(wl + SG::oS), *aT = dT + G * TK;
+        float *dummy = (float *)(wl + SG::oDummy);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int g = 4 * s_h + e;
+            const bool in = s_tok_in && u * G + g < ngroups;
+            *(s_on ? dT + g * TK + s_tok : dummy) = in ? sd[e] : 0.f;
+            if constexpr (T::kAux) *(s_on ? aT + g * TK + s_tok : dummy + 1) = in ? T::stage_aux(sd[e], ss[e]) : 0.f;
+        }
     };
 
-    float acc[RT][4];
-    v4f cm[RT];  // Q4_K min term
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        cm[t] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
+    // The lane's weight row within the set and its activation record: token
+    // c % TK of row set c / TK, the zero record for the other set.
+    const int wrow = L.c + 16 * L.s;
+    const bool areal = L.c / TK == L.s;
+    const int atok = L.c % TK;
+    const uint8_t *ar = wl + (areal ? SG::oA + atok * SG::kARow : SG::oZero) + 8 * L.r;
+    if constexpr (PK == 2) {
+        if (lane < UE / 16) *(uint4 *)(wl + SG::oZero + 16 * lane) = make_uint4(0u, 0u, 0u, 0u);
     }
-    auto step = [&](const typename T::Frag (&f)[RT], const ActUnit<T> &x, int u) {
-        T::template accumulate<RT>(f, x.a, sl, u * G, q, r16, acc, cm);
-    };
+    const ScaleLds<PK> sl{(const float *)(wl + SG::oS), (const float *)(wl + SG::oS) + G * TK};
 
-    typename T::Frag fa[RT], fb[RT];
-    ActUnit<T> xa, xb;
-#ifdef M27Q_MFMA_STAGGER
-    const int rot = nu > 0 ? (int)(blockIdx.x % (unsigned)nu) : 0;
-#else
-    const int rot = 0;
-#endif
-    auto uid = [&](int k) {
-        const int v = k + rot;
-        return ub + (v >= nu ? v - nu : v);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, u4[4] = {0.f, 0.f, 0.f, 0.f};
+    v4f cm = v4f{0.f, 0.f, 0.f, 0.f};  // Q4_K min term
+    auto compute = [&]() __attribute__((always_inline)) {
+        typename T::template Frag<PK> f0, f1;
+        AFrag<PK> x0, x1;
+        T::template load<PK>(f0, wl, wrow, L.r, 0, SG::kSide);
+        load_act<PK>(x0, ar, 0);
+        if constexpr (NS == 2) {
+            T::template load<PK>(f1, wl, wrow, L.r, 1, SG::kSide);
+            load_act<PK>(x1, ar, 1);
+        }
+        compute_half<T, PK, 0>(f0, x0, sl, 0, L, areal, atok, acc, u4, cm);
+        if constexpr (NS == 2) compute_half<T, PK, 1>(f1, x1, sl, 0, L, areal, atok, acc, u4, cm);
     };
-    const int u_first = nu > 0 ? uid(0) : min(ub, p.upr - 1);
-    load_w(fa, u_first);
-    load_act(xa, u_first);
-    int k = 0;
-    for (; k + 2 < nu; k += 2) {
-        load_w(fb, uid(k + 1));
-        load_act(xb, uid(k + 1));
-        step(fa, xa, uid(k));
-        load_w(fa, uid(k + 2));
-        load_act(xa, uid(k + 2));
-        step(fb, xb, uid(k + 1));
-    }
-    if (k + 1 < nu) {
-        load_w(fb, uid(k + 1));
-        load_act(xb, uid(k + 1));
-        step(fa, xa, uid(k));
-        step(fb, xb, uid(k + 1));
-    } else if (k < nu) {
-        step(fa, xa, uid(k));
+    // Loads are unconditional inside the loop (a conditional reload makes the
+    // compiler wait for every load before each use); the last unit is peeled.
+    // A wave's LDS reads and writes are executed in order, so a unit's
+    // staging writes follow the previous unit's operand reads.
+    if (nu > 0) {
+        issue(ub);
+        commit(ub);
+        for (int k = 0; k + 1 < nu; ++k) {
+            issue(ub + k + 1);
+            compute();
+            commit(ub + k + 1);
+        }
+        compute();
     }
     if (T::kAux) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[t][e] -= cm[t][e];
+        for (int e = 0; e < 4; ++e) acc[e] -= cm[e];
     }
 
-    // Partials of this wave's K slice -> LDS, then one thread per (token, row).
-#pragma unroll
-    for (int t = 0; t < RT; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[((size_t)wave * kMmaTok + 4 * q + e) * TR + 16 * t + r16] = acc[t][e];
+    // Partials of this wave's K slice -> LDS (over the staging areas), then
+    // one thread per (lane, e) adds the KS waves in a fixed order.
     __syncthreads();
-    for (int idx = (int)threadIdx.x; idx < M * TR; idx += KS * kWave) {
-        const int tok = idx / TR, rr = idx % TR, row = row0 + rr;
-        float v = red[(size_t)tok * TR + rr];
+    float *red = (float *)smem;  // [KS][4][64]
 #pragma unroll
-        for (int w = 1; w < KS; ++w) v += red[((size_t)w * kMmaTok + tok) * TR + rr];
-        if (row < rc) {
+    for (int e = 0; e < 4; ++e) red[(wave * 4 + e) * kWave + lane] = acc[e];
+    __syncthreads();
+    for (int idx = (int)threadIdx.x; idx < 4 * kWave; idx += KS * kWave) {
+        const int e = idx / kWave, ln = idx % kWave;
+        float v = red[idx];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) v += red[(w * 4 + e) * kWave + ln];
+        const Lane<PK> O(ln);
+        const int row = row0 + O.c + 16 * O.s, tok = 4 * O.r + e;
+        if (row < rc && tok < Mloc) {
             const size_t o = (size_t)(m0 + tok) * rc + row;
             p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
         }
     }
 }
 
-template <class T, int KS, int RT>
-static size_t mfma_lds(int upr) {
-    return (size_t)upr * T::kGroups * kMmaTok * (T::kAux ? 8 : 4) + (size_t)KS * kMmaTok * 16 * RT * 4;
+template <class T, int PK, int KS>
+static size_t mfma_lds(int) {
+    return (size_t)KS * Stage<T, PK>::kBytes;
 }
 
-template <class T, int KS, int RT>
-static hipError_t launch_mfma_t(MatmulMultiParams p, hipStream_t s) {
-    const size_t lds = mfma_lds<T, KS, RT>(p.upr);
+template <class T, int PK, int KS>
+static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
+    const size_t lds = mfma_lds<T, PK, KS>(p.upr);
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
         p.wg_start[i] = total;
-        total += (p.rc[i] + 16 * RT - 1) / (16 * RT);
+        total += (p.rc[i] + 16 * PK - 1) / (16 * PK);
     }
     p.wg_start[p.nmat] = total;
-    for (int m0 = 0; m0 < p.M; m0 += kMmaTok) {
-        hipLaunchKernelGGL((k_matmul_mfma<T, KS, RT>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
-        const hipError_t e = hipGetLastError();
+    hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
+    return hipGetLastError();
+}
+
+// Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 16: a
+// launch of fewer than 320 row sets (q/k/v, o and down with two-set tiles)
+// splits K over 8 waves, a larger one over 4; more waves per set cost more
+// than they hide.  Two row sets per tile whenever at most 8 tokens are left
+// and the product has at least 128 sets of 32 rows (every product of the
+// layer): down at M = 8 takes 21.7 us against 28.8 with one-set tiles.
+#ifndef M27Q_MM_KS
+#define M27Q_MM_KS 0
+#endif
+#ifndef M27Q_MM_PK2_MIN_SETS
+#define M27Q_MM_PK2_MIN_SETS 128
+#endif
+template <class T, int PK>
+static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
+    long long sets = 0;
+    for (int i = 0; i < p.nmat; ++i) sets += (p.rc[i] + 16 * PK - 1) / (16 * PK);
+    const int ks = M27Q_MM_KS ? M27Q_MM_KS : sets < 320 ? 8 : 4;
+    switch (ks) {
+        case 2: return launch_mfma_t<T, PK, 2>(p, m0, s);
+        case 8: return launch_mfma_t<T, PK, 8>(p, m0, s);
+        default: return launch_mfma_t<T, PK, 4>(p, m0, s);
+    }
+}
+
+template <class T>
+static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
+    long long sets32 = 0;
+    for (int i = 0; i < p.nmat; ++i) sets32 += (p.rc[i] + 31) / 32;
+    for (int m0 = 0; m0 < p.M;) {
+        const int left = p.M - m0;
+        const bool pk2 = left <= 8 && sets32 >= M27Q_MM_PK2_MIN_SETS;
+        const hipError_t e = pk2 ? launch_mfma_pk<T, 2>(p, m0, s) : launch_mfma_pk<T, 1>(p, m0, s);
         if (e != hipSuccess) return e;
+        m0 += pk2 ? Pack<2>::TK : Pack<1>::TK;
     }
     return hipSuccess;
 }
 
-// Launch shape: RT 16-row tiles per wave share each activation load and LDS
-// scale read; K is split over KS waves so that a launch still has a few
-// thousand waves.  KS * RT <= 16 keeps the LDS within the KS = 16, RT = 1 size
-// the caller checks.
 template <class T>
-static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
-#if defined(M27Q_MFMA_KS) && defined(M27Q_MFMA_RT)
-    static_assert(M27Q_MFMA_KS * M27Q_MFMA_RT <= 16, "LDS bound");
-    return launch_mfma_t<T, M27Q_MFMA_KS, M27Q_MFMA_RT>(p, s);
-#else
-    // Measured on the Qwen-27B layer (M = 2 .. 16): (4, 2) for gate/up
-    // (2176 tiles) and down (320 tiles, Q6_K), (8, 2) for q/k/v and o (512
-    // and 320 tiles, Q4_K); RT = 4 runs at one wave per SIMD.
-    long long tiles = 0;
-    for (int i = 0; i < p.nmat; ++i) tiles += (p.rc[i] + 15) / 16;
-    if (tiles >= 1024 || (std::is_same<T, MmaQ6K>::value && tiles >= 256)) return launch_mfma_t<T, 4, 2>(p, s);
-    if (tiles >= 256) return launch_mfma_t<T, 8, 2>(p, s);
-    return launch_mfma_t<T, 16, 1>(p, s);
-#endif
+static size_t mfma_lds_max() {
+    return std::max(mfma_lds<T, 1, 8>(0), mfma_lds<T, 2, 8>(0));
 }
 
-size_t matmul_mfma_lds_bytes(uint32_t type, int upr) {
+size_t matmul_mfma_lds_bytes(uint32_t type, int) {
+    // the largest over the shapes the selection can return (KS = 8)
     switch (type) {
-        case kQ4_K: return mfma_lds<MmaQ4K, 16, 1>(upr);
-        case kQ5_K: return mfma_lds<MmaQ5K, 16, 1>(upr);
-        case kQ6_K: return mfma_lds<MmaQ6K, 16, 1>(upr);
-        case kQ8_0: return mfma_lds<MmaQ80, 16, 1>(upr);
-        case kIQ4_XS: return mfma_lds<MmaIQ4XS, 16, 1>(upr);
+        case kQ4_K: return mfma_lds_max<MmQ4K>();
+        case kQ5_K: return mfma_lds_max<MmQ5K>();
+        case kQ6_K: return mfma_lds_max<MmQ6K>();
+        case kQ8_0: return mfma_lds_max<MmQ80>();
+        case kIQ4_XS: return mfma_lds_max<MmIQ4XS>();
         default: return 0;
     }
 }
 
 hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_mfma_cfg<MmaQ4K>(p, s);
-        case kQ5_K: return launch_mfma_cfg<MmaQ5K>(p, s);
-        case kQ6_K: return launch_mfma_cfg<MmaQ6K>(p, s);
-        case kQ8_0: return launch_mfma_cfg<MmaQ80>(p, s);
-        case kIQ4_XS: return launch_mfma_cfg<MmaIQ4XS>(p, s);
+        case kQ4_K: return launch_mfma_cfg<MmQ4K>(p, s);
+        case kQ5_K: return launch_mfma_cfg<MmQ5K>(p, s);
+        case kQ6_K: return launch_mfma_cfg<MmQ6K>(p, s);
+        case kQ8_0: return launch_mfma_cfg<MmQ80>(p, s);
+        case kIQ4_XS: return launch_mfma_cfg<MmIQ4XS>(p, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -14,8 +14,8 @@ CASES = [  # type, rows, K, M, layout
     ("Q4_K", 40, 512, 5, 0), ("Q4_K", 40, 512, 64, 1),
     ("Q6_K", 5120, 17408, 16, 1), ("Q6_K", 5120, 17408, 3, 0), ("Q6_K", 24, 768, 9, 1),
     ("Q8_0", 2048, 6144, 16, 1), ("Q8_0", 2048, 6144, 2, 0), ("Q8_0", 13, 160, 7, 1),
-    # few-token GEMV path (M <= 4, TILED): a padding token (M = 3), partial
-    # 8-row tiles, each type
+    # few tokens: M = 2 on the GEMV-structured kernel, M = 3 and 4 on MFMA
+    # (padding tokens, partial 8-row tiles), each type
     ("Q6_K", 5120, 17408, 2, 1), ("Q6_K", 24, 768, 4, 1), ("Q4_K", 40, 512, 3, 1), ("Q8_0", 13, 160, 3, 1),
     ("Q8_0", 2048, 6144, 4, 1),
     # Q5_K on each path: few-token GEMV, MFMA, GGUF VALU
@@ -23,6 +23,12 @@ CASES = [  # type, rows, K, M, layout
     # IQ4_XS likewise
     ("IQ4_XS", 6144, 5120, 2, 1), ("IQ4_XS", 6144, 5120, 16, 1), ("IQ4_XS", 40, 512, 9, 1),
     ("IQ4_XS", 40, 512, 3, 0),
+    # MFMA with two 16-row sets per tile (M <= 8 and >= 128 sets of 32 rows):
+    # a partial last set (8200 rows), a partial Q8_0 unit (K = 160), every
+    # type, and 24 tokens (one 16-token launch, then one packed 8-token launch)
+    ("Q4_K", 8200, 512, 5, 1), ("Q4_K", 8192, 512, 8, 1), ("Q4_K", 8192, 512, 24, 1),
+    ("Q6_K", 8200, 768, 7, 1), ("Q8_0", 8200, 160, 6, 1), ("Q5_K", 8192, 512, 8, 1),
+    ("IQ4_XS", 8200, 512, 6, 1),
 ]
 
 
