@@ -29,14 +29,18 @@
 // With PK = 2 each MFMA m covers positions 16 m .. 16 m + 15, which keeps
 // the two Q6_K sub-blocks apart.
 //
-// Weights are read from the TILED layout half a unit (four groups) at a time,
-// double buffered; activation codes come from the quantized activation buffer
-// (L1/L2 hits: every wave at the same K reads the same bytes), zero operand
-// lanes from a table of zeros; activation scales are staged in LDS,
-// transposed to [group][token] so a lane reads its 4 tokens at once.  K is
-// split over the KS waves of a workgroup, one row set per workgroup, and the
-// KS partials are added in LDS in a fixed order.  Padding tokens (past M) read
-// a real token's codes; their scales are zero and their outputs are dropped.
+// Data movement.  The operand layouts above would need 8-byte loads that
+// each touch 16 rows (or 16 token rows K bytes apart); measured on gfx950,
+// such loads stall in the L1 tag lookup and bound the kernel well below the
+// HBM rate.  So each wave streams its K slice one TILED unit at a time with
+// 16-byte loads of contiguous bytes (the set's weight tiles, the tokens'
+// codes and scales), issued while the previous unit computes, writes them to
+// its own LDS area (padded row and token records, so the operand reads below
+// are free of bank conflicts), and reads the MFMA operands from there.  The
+// zero operand lanes read a zero record.  K is split over the KS waves of a
+// workgroup, one row set per workgroup, and the KS partials are added in LDS
+// in a fixed order.  Padding tokens (past M) read a real token's codes; their
+// scales are zero and their outputs are dropped.
 //
 // No reference counterpart: the reference runs prefill and decode one token at
 // a time (src/mono27b_chat.cpp:399-403).
@@ -51,10 +55,6 @@ namespace m27q {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // staging registers (promoted; HIP's uint4 arrays are not)
-
-// Operand bytes of padding lanes: every offset a zero lane reads within one
-// unit (< 264 bytes) lands here.
-__device__ __align__(16) int8_t kMmZero[512] = {};
 
 template <int PK>
 struct Pack {
