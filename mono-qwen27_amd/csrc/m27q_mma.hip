@@ -474,8 +474,11 @@ struct Stage {
 // while the previous unit computes), written to the wave's LDS area, read
 // back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
+#ifndef M27Q_MM_WPE
+#define M27Q_MM_WPE 3
+#endif
 template <class T, int PK, int KS>
-__global__ __launch_bounds__(kWave *KS, 3) void k_matmul_mfma(MatmulMultiParams p, int m0) {
+__global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     using SG = Stage<T, PK>;
     constexpr int G = T::kGroups, NS = T::kSteps, TK = Pack<PK>::TK, UE = SG::UE, UB = SG::UB;
