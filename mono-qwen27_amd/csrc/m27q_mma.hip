@@ -505,7 +505,10 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
 
     // Staging map of this lane: weight chunks (tiles past the end reread the
     // last tile), activation chunks (padding tokens read token m0), scales.
-    size_t goff[SG::kNW];
+    // 32-bit offsets from a workgroup-uniform base: the loads take the
+    // scalar-base form, with no per-lane 64-bit address arithmetic (a TILED
+    // matrix is below 4 GiB: the host checks it).
+    uint32_t goff[SG::kNW];
     int wdst[SG::kNW];
 #pragma unroll
     for (int n = 0; n < SG::kNW; ++n) {
@@ -513,22 +516,22 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
         const bool ok = id < SG::kWChunks;
         const int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
         const int tile = min(row0 / kTileRows + t, ntiles8 - 1);
-        goff[n] = (size_t)tile * p.upr * UB + 16 * c;
+        goff[n] = (uint32_t)tile * (uint32_t)(p.upr * UB) + 16u * c;
         wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
     }
-    size_t aoff[SG::kNA];
+    uint32_t aoff[SG::kNA];
     int adst[SG::kNA];
 #pragma unroll
     for (int n = 0; n < SG::kNA; ++n) {
         const int id = n * kWave + lane;
         const int tok = id / (UE / 16), c = id % (UE / 16);
-        aoff[n] = (size_t)(m0 + (tok < Mloc ? tok : 0)) * p.K + 16 * c;
+        aoff[n] = (uint32_t)(m0 + (tok < Mloc ? tok : 0)) * (uint32_t)p.K + 16u * c;
         adst[n] = SG::oA + tok * SG::kARow + 16 * c;
     }
     const int s_tok = lane / (G / 4), s_h = lane % (G / 4);
     const bool s_on = lane < SG::kSLanes;
     const bool s_tok_in = s_on && s_tok < Mloc;
-    const size_t s_row = (size_t)(m0 + (s_tok_in ? s_tok : 0)) * ngroups;
+    const uint32_t s_row = (uint32_t)(m0 + (s_tok_in ? s_tok : 0)) * (uint32_t)ngroups + 4u * s_h;
 
     v4u rw[SG::kNW], ra[SG::kNA];
     float sd[4];
@@ -538,15 +541,15 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
         for (int n = 0; n < SG::kNW; ++n) rw[n] = *(const v4u *)(Wm + (size_t)u * UB + goff[n]);
 #pragma unroll
         for (int n = 0; n < SG::kNA; ++n) ra[n] = *(const v4u *)(p.xq + (size_t)u * UE + aoff[n]);
-        const int g0 = u * G + 4 * s_h;
+        const float *xd = p.xd + (size_t)u * G;
         if constexpr (G == 8) {  // whole units: rows of 8 k groups, 16-byte aligned
-            const float4 d = *(const float4 *)(p.xd + s_row + g0);
+            const float4 d = *(const float4 *)(xd + s_row);
             sd[0] = d.x;
             sd[1] = d.y;
             sd[2] = d.z;
             sd[3] = d.w;
             if constexpr (T::kAux) {
-                const uint4 v = *(const uint4 *)(p.xs + s_row + g0);
+                const uint4 v = *(const uint4 *)(p.xs + (size_t)u * G + s_row);
                 ss[0] = v.x;
                 ss[1] = v.y;
                 ss[2] = v.z;
@@ -554,7 +557,7 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
             }
         } else {  // Q8_0: the last unit can pass K
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sd[e] = p.xd[s_row + min(g0 + e, ngroups - 1)];
+            for (int e = 0; e < 4; ++e) sd[e] = p.xd[s_row + min(u * G + e, ngroups - 1)];  // s_h = 0
         }
     };
     auto commit = [&](int u) __attribute__((always_inline)) {
@@ -567,7 +570,7 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int g = 4 * s_h + e;
-            const bool in = s_tok_in && u * G + g < ngroups;
+            const bool in = s_tok_in && (G == 8 || u * G + g < ngroups);  // K-quant units are whole
             *(s_on ? dT + g * TK + s_tok : dummy) = in ? sd[e] : 0.f;
             if constexpr (T::kAux) *(s_on ? aT + g * TK + s_tok : dummy + 1) = in ? T::stage_aux(sd[e], ss[e]) : 0.f;
         }
