@@ -390,6 +390,9 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfg81: return launch_q8_cfg<T, LAYOUT, Cfg81, SWIGLU, XF32>(p, s);
         case kCfg42: return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
         case kCfg84: return launch_q8_cfg<T, LAYOUT, Cfg84, SWIGLU, XF32>(p, s);
+        case kCfg161:  // chosen for small products without the SwiGLU epilogue only
+            if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg161, SWIGLU, XF32>(p, s);
+            return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
         default: return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     }
 }
@@ -419,6 +422,7 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
         case kCfg42: return lds_sw<T, Cfg42>(upr, swiglu);
         case kCfg84: return lds_sw<T, Cfg84>(upr, swiglu);
         case kCfgQ: return lds_sw<T, CfgQ>(upr, swiglu);
+        case kCfg161: return swiglu ? lds_sw<T, Cfg41>(upr, swiglu) : lds_sw<T, Cfg161>(upr, swiglu);
         default: return lds_sw<T, Cfg41>(upr, swiglu);
     }
 }
@@ -440,6 +444,7 @@ int gemv_q8_tiles_per_wg(int cfg) {
         case kCfg42: return Cfg42::TPW;
         case kCfg84: return Cfg84::TPW;
         case kCfgQ: return CfgQ::TPW;
+        case kCfg161: return Cfg161::TPW;
         default: return Cfg41::TPW;
     }
 }

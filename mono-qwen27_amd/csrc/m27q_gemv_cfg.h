@@ -18,8 +18,12 @@
 //   down 5120 x 17408 Q6_K                   (4,1) 21.30 us      (4,1) 17.09 us
 //   gate/up + fused output quantization      (2,4,1) 24.55 us    (2,4,1) 23.38 us
 //   Q4_K 17408 x 5120 alone                  (4,2) 11.92 us
-//   LM head Q6_K 248320 x 5120               (4,2) 165.2 us (6.31 TB/s)
-// (shapes written (KS, TPW) have WT = TPW).
+//   LM head Q6_K 248320 x 5120               (4,2) 164.1 us (6.36 TB/s)
+//   Q8_0 2048 x 2048 (draft)                 (16,1) 3.43 us, (8,1) 3.70, (8,4) 4.32
+//   Q8_0 6144 x 2048 (draft)                 (8,1)  4.83 us, (8,4) 5.12, (16,1) 6.78
+//   Q8_0 2048 x 6144 (draft)                 (16,1) 5.26 us, (8,1) 5.78, (4,1) 6.80
+// (shapes written (KS, TPW) have WT = TPW).  Small products need more waves
+// per row than their row count provides: 2048 rows are 256 tiles, one per CU.
 //
 // Products that quantize their output (yq) need whole 32-row groups per
 // workgroup (TPW >= 4) and use CfgQ.  GGUF-layout weights (the compatibility
@@ -51,26 +55,31 @@ struct GemvCfg {
 #ifndef M27Q_CFG_Q
 #define M27Q_CFG_Q 2, 4, 1
 #endif
+#ifndef M27Q_CFG_161
+#define M27Q_CFG_161 16, 1, 1
+#endif
 
 using Cfg41 = GemvCfg<M27Q_CFG_41>;
 using Cfg81 = GemvCfg<M27Q_CFG_81>;
 using Cfg42 = GemvCfg<M27Q_CFG_42>;
 using Cfg84 = GemvCfg<M27Q_CFG_84>;
 using CfgQ = GemvCfg<M27Q_CFG_Q>;
+using Cfg161 = GemvCfg<M27Q_CFG_161>;
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
 
-enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4 };
+enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) over upr units per row.
 inline int pick_gemv_cfg(bool tiled, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
     if (out_quant) return kCfgQ;
     if (!tiled) return kCfg41;
-    if (upr >= 40) return kCfg41;
-    if (swiglu) return xf32 ? kCfg41 : kCfg81;
+    if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
+    if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
         if (upr >= 24) return kCfg81;
-        return xf32 ? kCfg84 : kCfg41;
+        if (!xf32) return kCfg41;
+        return rows_total <= 2048 ? kCfg161 : rows_total <= 6144 ? kCfg81 : kCfg84;
     }
     return kCfg42;
 }

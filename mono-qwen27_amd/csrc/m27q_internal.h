@@ -36,8 +36,8 @@ struct GemvParams {
     uint32_t *os;
 };
 
-// Integer-dot GEMV (m27q_gemv.hip).  cfg: kCfgShortK / kCfgMidK / kCfgLongK
-// (m27q_gemv_cfg.h).  The grid is p.wg_start[p.nmat] workgroups.  The
+// Integer-dot GEMV (m27q_gemv.hip).  cfg: a launch shape of m27q_gemv_cfg.h
+// (pick_gemv_cfg).  The grid is p.wg_start[p.nmat] workgroups.  The
 // activation is p.x (fp32, quantized in the kernel) when not NULL, else p.xq.
 size_t gemv_q8_lds_bytes(uint32_t type, int upr, bool swiglu, int cfg);
 int gemv_q8_tiles_per_wg(int cfg);
