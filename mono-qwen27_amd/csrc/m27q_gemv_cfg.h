@@ -16,7 +16,8 @@
 //   o 5120 x 6144 Q4_K                       (8,1)  6.77 us      (8,1) 6.01 us
 //   gate/up SwiGLU 2 x 17408 x 5120 Q4_K     (4,1) 20.91 us      (8,1) 20.19 us
 //   down 5120 x 17408 Q6_K                   (4,1) 21.30 us      (4,1) 17.09 us
-//   gate/up + fused output quantization      (2,4,1) 24.55 us    (2,4,1) 23.38 us
+//   gate/up + fused output quantization      (2,4,2) 24.2 us (2,4,1) 24.85, (4,4,4) 24.4,
+//                                            (1,4,1) 24.65, (4,4,1) 26.3, (2,4,4) 26.9
 //   Q4_K 17408 x 5120 alone                  (4,2) 11.92 us
 //   LM head Q6_K 248320 x 5120               (4,2) 164.1 us (6.36 TB/s)
 //   Q8_0 2048 x 2048 (draft)                 (16,1) 3.43 us, (8,1) 3.70, (8,4) 4.32
@@ -53,7 +54,7 @@ struct GemvCfg {
 #define M27Q_CFG_84 8, 4, 4
 #endif
 #ifndef M27Q_CFG_Q
-#define M27Q_CFG_Q 2, 4, 1
+#define M27Q_CFG_Q 2, 4, 2
 #endif
 #ifndef M27Q_CFG_161
 #define M27Q_CFG_161 16, 1, 1
