@@ -29,6 +29,9 @@ CASES = [  # type, rows, K, M, layout
     ("Q4_K", 8200, 512, 5, 1), ("Q4_K", 8192, 512, 8, 1), ("Q4_K", 8192, 512, 24, 1),
     ("Q6_K", 8200, 768, 7, 1), ("Q8_0", 8200, 160, 6, 1), ("Q5_K", 8192, 512, 8, 1),
     ("IQ4_XS", 8200, 512, 6, 1),
+    # gate-sized rows at M = 3 (two sets per tile), the down shape at M = 12
+    # (padding tokens in a 16-token launch), 17 tokens (16, then 1 on two sets)
+    ("Q4_K", 17408, 5120, 3, 1), ("Q6_K", 5120, 17408, 12, 1), ("Q4_K", 8192, 512, 17, 1),
 ]
 
 
@@ -57,7 +60,7 @@ def test_matmul_vs_oracle(m27q, ora, dev, type_name, rc, k, M, layout):
         assert (np.abs(got[m] - want) <= int_dot_tol(nrm) + 1e-6 * np.abs(res[m])).all(), m
 
 
-@pytest.mark.parametrize("M", [2, 16, 19])
+@pytest.mark.parametrize("M", [2, 5, 16, 19])
 def test_matmul_multi_vs_oracle(m27q, ora, dev, M):
     """q/k/v-shaped weights on one activation in one launch, each against the
     integer-dot oracle (row subsets), across the 16-token launch boundary."""
