@@ -204,6 +204,25 @@ def suite(m27q, torch, dev, layers, reps):
     us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids[c], rows, stream=st), 16, reps)
     out["cfg5_gather_512_q6k_rows"] = {"us": round(us, 3), "GBps": round((512 * 4200 + 512 * 5120 * 4) / us / 1e3, 1)}
     log("config 5 done")
+    # A decode step of linears, one graph with nothing on the host in between:
+    # the embedding row of one token id (the 248320 x 5120 Q6_K table stands in
+    # for token_embd), 64 layers of the layer's four products over the rotated
+    # cold copies, the LM head, the exact top-64 and the on-device sample.
+    B = Buffers(m27q, dev)
+    tok_id = torch.tensor([12345], dtype=torch.int32, device=dev)
+    u = torch.full((1,), 0.3, dtype=torch.float32, device=dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+
+    def decode_step(c, st):
+        m27q.embed_rows(lm, tok_id, B.x.view(1, 5120), stream=st)
+        for li in range(64):
+            layer_pass(m27q, layers[li % len(layers)], B, st)
+        m27q.matvec(lm, B.out, logits, stream=st)
+        m27q.topk(logits, k, idx, val, scratch, stream=st)
+        m27q.sample(idx, val, k, 0.8, 0.05, 0.95, u, tok, stream=st)
+    us = timed(torch, decode_step, 1, max(4, reps // 10))
+    out["decode_step_linears_64_layers"] = {"us": round(us, 1), "tokens_per_s": round(1e6 / us, 1)}
+    log(f"decode step of linears: {us:.1f} us")
     return out
 
 
