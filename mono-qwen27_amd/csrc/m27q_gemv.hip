@@ -33,6 +33,8 @@
 // :2022-2030) and the fp32 fallbacks k_q4k_mv / k_q6k_mt / k_q80_mv / k_f16_mv
 // / k_f32_mv / k_q5k_mv / k_iq4xs_mv (exec:920-951, :1053-1072, :1076-1096,
 // :899-916, :1100-1114, :953-985, :992-1020).
+#include <algorithm>
+
 #include "m27q_gemv_cfg.h"
 #include "m27q_internal.h"
 #include "m27q_types.h"
@@ -393,6 +395,10 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfg161:  // chosen for small products without the SwiGLU epilogue only
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg161, SWIGLU, XF32>(p, s);
             return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
+        case kCfg822:  // fp32-input products without the SwiGLU epilogue only; the
+                       // other instantiation keeps the tiles per workgroup the grid was sized for
+            if constexpr (!SWIGLU && XF32) return launch_q8_cfg<T, LAYOUT, Cfg822, SWIGLU, XF32>(p, s);
+            return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
         default: return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     }
 }
@@ -423,6 +429,7 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
         case kCfg84: return lds_sw<T, Cfg84>(upr, swiglu);
         case kCfgQ: return lds_sw<T, CfgQ>(upr, swiglu);
         case kCfg161: return swiglu ? lds_sw<T, Cfg41>(upr, swiglu) : lds_sw<T, Cfg161>(upr, swiglu);
+        case kCfg822: return std::max(lds_sw<T, Cfg42>(upr, swiglu), lds_sw<T, Cfg822>(upr, swiglu));
         default: return lds_sw<T, Cfg41>(upr, swiglu);
     }
 }
@@ -445,6 +452,7 @@ int gemv_q8_tiles_per_wg(int cfg) {
         case kCfg84: return Cfg84::TPW;
         case kCfgQ: return CfgQ::TPW;
         case kCfg161: return Cfg161::TPW;
+        case kCfg822: return Cfg822::TPW;
         default: return Cfg41::TPW;
     }
 }

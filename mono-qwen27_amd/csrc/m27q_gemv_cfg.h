@@ -13,7 +13,8 @@
 //
 //   product (TILED)                          fp32 x in           quantized x in
 //   q/k/v 6144+1024+1024 x 5120 Q4_K         (8,4)  7.00 us      (4,1) 6.69 us
-//   o 5120 x 6144 Q4_K                       (8,1)  6.77 us      (8,1) 6.01 us
+//   o 5120 x 6144 Q4_K                       (8,2,2) 7.51 us     (8,1) 6.01 us
+//                                            (8,1) 7.88, (6,2,1) 7.98, (4,2,2) 8.24
 //   gate/up SwiGLU 2 x 17408 x 5120 Q4_K     (4,1) 20.91 us      (8,1) 20.19 us
 //   down 5120 x 17408 Q6_K                   (4,1) 21.30 us      (4,1) 17.09 us
 //   gate/up + fused output quantization      (2,4,2) 24.2 us (2,4,1) 24.85, (4,4,4) 24.4,
@@ -59,6 +60,9 @@ struct GemvCfg {
 #ifndef M27Q_CFG_161
 #define M27Q_CFG_161 16, 1, 1
 #endif
+#ifndef M27Q_CFG_822
+#define M27Q_CFG_822 8, 2, 2
+#endif
 
 using Cfg41 = GemvCfg<M27Q_CFG_41>;
 using Cfg81 = GemvCfg<M27Q_CFG_81>;
@@ -66,9 +70,11 @@ using Cfg42 = GemvCfg<M27Q_CFG_42>;
 using Cfg84 = GemvCfg<M27Q_CFG_84>;
 using CfgQ = GemvCfg<M27Q_CFG_Q>;
 using Cfg161 = GemvCfg<M27Q_CFG_161>;
+using Cfg822 = GemvCfg<M27Q_CFG_822>;
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
+static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 
-enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5 };
+enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) over upr units per row.
@@ -78,7 +84,7 @@ inline int pick_gemv_cfg(bool tiled, bool xf32, bool swiglu, bool out_quant, lon
     if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
     if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
-        if (upr >= 24) return kCfg81;
+        if (upr >= 24) return xf32 ? kCfg822 : kCfg81;
         if (!xf32) return kCfg41;
         return rows_total <= 2048 ? kCfg161 : rows_total <= 6144 ? kCfg81 : kCfg84;
     }
