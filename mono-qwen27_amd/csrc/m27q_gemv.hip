@@ -384,9 +384,6 @@ static hipError_t launch_q8_cfg(const GemvParams &p, hipStream_t s) {
 
 template <class T, int LAYOUT, bool SWIGLU, bool XF32>
 static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
-    if constexpr (LAYOUT == M27Q_LAYOUT_GGUF)
-        return cfg == kCfgQ ? launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s)
-                            : launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     switch (cfg) {
         case kCfgQ: return launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s);
         case kCfg81: return launch_q8_cfg<T, LAYOUT, Cfg81, SWIGLU, XF32>(p, s);

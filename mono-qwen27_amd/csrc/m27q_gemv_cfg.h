@@ -29,8 +29,10 @@
 //
 // Products that quantize their output (yq) need whole 32-row groups per
 // workgroup (TPW >= 4) and use CfgQ.  GGUF-layout weights (the compatibility
-// path) use one shape.  Each can be overridden at build time
-// (-DM27Q_CFG_41=KS,TPW,WT ...) to sweep.
+// path) follow the same rules: q/k/v 7.97 us and o 7.83 with them against 8.66
+// and 8.20 on (4,1) alone; gate/up and down pay for the row-major blocks
+// (30.6 and 21.6 us against 24.2 and 16.4 TILED).  Each shape can be
+// overridden at build time (-DM27Q_CFG_41=KS,TPW,WT ...) to sweep.
 #pragma once
 
 namespace m27q {
@@ -78,9 +80,8 @@ enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, k
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) over upr units per row.
-inline int pick_gemv_cfg(bool tiled, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
+inline int pick_gemv_cfg(bool /*tiled*/, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
     if (out_quant) return kCfgQ;
-    if (!tiled) return kCfg41;
     if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
     if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
