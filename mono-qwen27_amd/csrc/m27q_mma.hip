@@ -94,19 +94,21 @@ struct ScaleLds {
     __device__ float4 dx(int g, int r) const { return *(const float4 *)(dT + g * Pack<PK>::TK + 4 * r); }
 };
 
-// Activation operands of one half unit: a[group][piece].
-template <int PK>
+// Activation operands of one half unit: a[group][piece], NP pieces per group
+// (the policy's kPieces: PK, or two zero-split views for Q6_K at PK = 1).
+template <int NP>
 struct AFrag {
-    uint2 a[4][PK];
+    uint2 a[4][NP];
 };
 
-// From the lane's token record in LDS (its piece offset 8 r included).
-template <int PK>
-__device__ __forceinline__ void load_act(AFrag<PK> &f, const uint8_t *ar, int st) {
+// Piece m of each group from base[m] (a token or zero record in LDS, the
+// lane's position offset included).
+template <int NP>
+__device__ __forceinline__ void load_act(AFrag<NP> &f, const uint8_t *const (&base)[NP], int st) {
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg)
 #pragma unroll
-        for (int m = 0; m < PK; ++m) f.a[jg][m] = ld8(ar + 32 * (4 * st + jg) + Pack<PK>::W8 * m);
+        for (int m = 0; m < NP; ++m) f.a[jg][m] = ld8(base[m] + 32 * (4 * st + jg));
 }
 
 // ------------------------------------------------------------ Q4_K, Q5_K --
@@ -117,6 +119,9 @@ struct MmQ4KT {
     static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
+    static constexpr bool kWide = Q5;  // more live registers than 3 waves per SIMD allow at PK = 2
+    template <int PK>
+    static constexpr int kPieces = PK;
     // The min term's token factor: dx * (sum of the 32 codes).
     __device__ static float stage_aux(float d, uint32_t s) { return d * (float)(s_lo(s) + s_hi(s)); }
     template <int PK>
@@ -206,6 +211,12 @@ struct MmQ6K {
     static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = kQ6KUnit;
     static constexpr bool kAux = false;
+    // S0 and S1 each take the activations of one 16-value sub-block: at
+    // PK = 1 two views of the group with the other half zero, at PK = 2 the
+    // group's two pieces
+    template <int PK>
+    static constexpr int kPieces = 2;
+    static constexpr bool kWide = true;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     template <int PK>
     struct Frag {
@@ -253,19 +264,15 @@ struct MmQ6K {
         return as_long(b0 ^ 0x80808080u, b1 ^ 0x80808080u);
     }
     // S0 / S1: the sums over the two 16-value sub-blocks.  PK = 1: quarters
-    // 0-1 hold sub-block 0, so two MFMAs with the other half of the weight
-    // operand zero; PK = 2: MFMA m covers sub-block m.
+    // 0-1 hold sub-block 0, so two MFMAs on the same weights, each with the
+    // activation view whose other half reads the zero record; PK = 2: MFMA m
+    // covers sub-block m.
     template <int PK, int ST>
-    __device__ static void mma(const Frag<PK> &f, const AFrag<PK> &a, int jg, const Lane<PK> &L, v4i &S0, v4i &S1) {
-        if constexpr (PK == 1) {
-            const long b = operand<PK>(f, jg, 0);
-            const bool lo = L.q < 2;
-            S0 = mfma32(as_long(a.a[jg][0]), lo ? b : 0l, v4i{0, 0, 0, 0});
-            S1 = mfma32(as_long(a.a[jg][0]), lo ? 0l : b, v4i{0, 0, 0, 0});
-        } else {
-            S0 = mfma32(as_long(a.a[jg][0]), operand<PK>(f, jg, 0), v4i{0, 0, 0, 0});
-            S1 = mfma32(as_long(a.a[jg][1]), operand<PK>(f, jg, 1), v4i{0, 0, 0, 0});
-        }
+    __device__ static void mma(const Frag<PK> &f, const AFrag<2> &a, int jg, const Lane<PK> &, v4i &S0, v4i &S1) {
+        const long b0 = operand<PK>(f, jg, 0);
+        const long b1 = PK == 1 ? b0 : operand<PK>(f, jg, PK - 1);
+        S0 = mfma32(as_long(a.a[jg][0]), b0, v4i{0, 0, 0, 0});
+        S1 = mfma32(as_long(a.a[jg][1]), b1, v4i{0, 0, 0, 0});
     }
     template <int PK, int ST>
     struct Half {
@@ -302,6 +309,9 @@ struct MmQ80 {
     static constexpr int kGroups = 4, kSteps = 1;  // four 32-blocks per TILED unit
     static constexpr int kUnitBytes = kQ80Unit;
     static constexpr bool kAux = false;
+    static constexpr bool kWide = false;
+    template <int PK>
+    static constexpr int kPieces = PK;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     template <int PK>
     struct Frag {
@@ -353,6 +363,9 @@ struct MmIQ4XS {
     static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = kIQ4XSUnit;
     static constexpr bool kAux = false;
+    static constexpr bool kWide = false;
+    template <int PK>
+    static constexpr int kPieces = PK;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     template <int PK>
     struct Frag {
@@ -412,7 +425,8 @@ struct IntTag {
 // One half unit: the four groups' MFMAs, each issued one group ahead of the
 // previous group's scale arithmetic.
 template <class T, int PK, int ST>
-__device__ __forceinline__ void compute_half(const typename T::template Frag<PK> &f, const AFrag<PK> &a,
+__device__ __forceinline__ void compute_half(const typename T::template Frag<PK> &f,
+                                             const AFrag<T::template kPieces<PK>> &a,
                                              const ScaleLds<PK> &sl, int gu, const Lane<PK> &L, bool areal, int atok,
                                              float (&acc)[4], float (&u)[4], v4f &cm) {
     const typename T::template Half<PK, ST> hs(f, sl, gu, L, areal, atok, cm);
@@ -441,7 +455,8 @@ __device__ __forceinline__ void compute_half(const typename T::template Frag<PK>
 // Per-wave LDS staging area for one unit (bytes):
 //   W: 16 PK row records of T::kRowBytes, then a side area (64 bytes per tile)
 //   A: TK token records of 32 G + 16 bytes (G groups of codes + pad), then,
-//      for PK = 2, one record of zeros for the operand lanes of the other set
+//      for PK = 2 (and Q6_K's zero-split views), one record of zeros for the
+//      operand lanes of the other set (or sub-block)
 //   S: dT [G][TK] and, for Q4_K, aT [G][TK] floats
 //   a 16-byte slot that absorbs the writes of lanes past the data
 // The paddings keep the MFMA-layout reads free of bank conflicts: the row
@@ -455,7 +470,8 @@ struct Stage {
     static constexpr int kARow = UE + 16;
     static constexpr int oA = kW;
     static constexpr int oZero = oA + TK * kARow;
-    static constexpr int oS = oZero + (PK == 2 ? UE : 0);
+    static constexpr bool kZeroRec = PK == 2 || T::template kPieces<PK> != PK;
+    static constexpr int oS = oZero + (kZeroRec ? UE : 0);
     static constexpr int oDummy = oS + G * TK * 4 * (T::kAux ? 2 : 1);
     static constexpr int kBytes = (oDummy + 16 + 15) / 16 * 16;
     static constexpr int kWChunks = 2 * PK * UB / 16;  // 16-byte chunks of the set's unit
@@ -474,11 +490,18 @@ struct Stage {
 // while the previous unit computes), written to the wave's LDS area, read
 // back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
+// Waves per SIMD the register budget is cut for: 3, or 2 where the two-set
+// fragments of Q5_K and Q6_K would spill at 3 (those launches have 160 row
+// sets for 256 CUs at the model's shapes, so the lower bound costs nothing).
 #ifndef M27Q_MM_WPE
-#define M27Q_MM_WPE 3
+#define M27Q_MM_WPE 0
 #endif
+template <class T, int PK>
+constexpr int mm_waves_per_eu() {
+    return M27Q_MM_WPE ? M27Q_MM_WPE : PK == 2 && T::kWide ? 2 : 3;
+}
 template <class T, int PK, int KS>
-__global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMultiParams p, int m0) {
+__global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmul_mfma(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     using SG = Stage<T, PK>;
     constexpr int G = T::kGroups, NS = T::kSteps, TK = Pack<PK>::TK, UE = SG::UE, UB = SG::UB;
@@ -582,7 +605,18 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
     const bool areal = L.c / TK == L.s;
     const int atok = L.c % TK;
     const uint8_t *ar = wl + (areal ? SG::oA + atok * SG::kARow : SG::oZero) + 8 * L.r;
-    if constexpr (PK == 2) {
+    constexpr int NP = T::template kPieces<PK>;
+    const uint8_t *ab[NP];
+    if constexpr (NP == PK) {
+#pragma unroll
+        for (int m = 0; m < NP; ++m) ab[m] = ar + Pack<PK>::W8 * m;
+    } else {  // Q6_K at PK = 1: quarters 0-1 (sub-block 0) and 2-3 (sub-block 1)
+        static_assert(PK == 1 && NP == 2, "zero-split activation views");
+        const uint8_t *z = wl + SG::oZero + 8 * L.r;
+        ab[0] = L.q < 2 ? ar : z;
+        ab[1] = L.q < 2 ? z : ar;
+    }
+    if constexpr (SG::kZeroRec) {
         if (lane < UE / 16) *(uint4 *)(wl + SG::oZero + 16 * lane) = make_uint4(0u, 0u, 0u, 0u);
     }
     const ScaleLds<PK> sl{(const float *)(wl + SG::oS), (const float *)(wl + SG::oS) + G * TK};
@@ -591,12 +625,12 @@ __global__ __launch_bounds__(kWave *KS, M27Q_MM_WPE) void k_matmul_mfma(MatmulMu
     v4f cm = v4f{0.f, 0.f, 0.f, 0.f};  // Q4_K min term
     auto compute = [&]() __attribute__((always_inline)) {
         typename T::template Frag<PK> f0, f1;
-        AFrag<PK> x0, x1;
+        AFrag<NP> x0, x1;
         T::template load<PK>(f0, wl, wrow, L.r, 0, SG::kSide);
-        load_act<PK>(x0, ar, 0);
+        load_act<NP>(x0, ab, 0);
         if constexpr (NS == 2) {
             T::template load<PK>(f1, wl, wrow, L.r, 1, SG::kSide);
-            load_act<PK>(x1, ar, 1);
+            load_act<NP>(x1, ab, 1);
         }
         compute_half<T, PK, 0>(f0, x0, sl, 0, L, areal, atok, acc, u4, cm);
         if constexpr (NS == 2) compute_half<T, PK, 1>(f1, x1, sl, 0, L, areal, atok, acc, u4, cm);
