@@ -490,15 +490,17 @@ struct Stage {
 // while the previous unit computes), written to the wave's LDS area, read
 // back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
-// Waves per SIMD the register budget is cut for: 3, or 2 where the two-set
-// fragments of Q5_K and Q6_K would spill at 3 (those launches have 160 row
-// sets for 256 CUs at the model's shapes, so the lower bound costs nothing).
+// Waves per SIMD the register budget is cut for, the most that compiles
+// without spills: one-set launches 4 (128 VGPRs; Q4_K gate/up at M = 16 runs
+// 2 us faster than at 3), two-set launches 3; Q5_K and Q6_K one less (their
+// two-set launches have 160 row sets for 256 CUs at the model's shapes, so
+// the lower occupancy costs nothing).
 #ifndef M27Q_MM_WPE
 #define M27Q_MM_WPE 0
 #endif
 template <class T, int PK>
 constexpr int mm_waves_per_eu() {
-    return M27Q_MM_WPE ? M27Q_MM_WPE : PK == 2 && T::kWide ? 2 : 3;
+    return M27Q_MM_WPE ? M27Q_MM_WPE : (PK == 2 ? 3 : 4) - (T::kWide ? 1 : 0);
 }
 template <class T, int PK, int KS>
 __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmul_mfma(MatmulMultiParams p, int m0) {
