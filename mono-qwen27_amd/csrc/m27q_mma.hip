@@ -73,6 +73,15 @@ __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; }
+// Raw buffer loads: a scalar base (the descriptor) and scalar offset, a 32-bit
+// per-lane offset, no per-lane address arithmetic.  The record count is the
+// buffer's size, so a read past it returns zeros and touches no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4u buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
 __device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
 __device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
 __device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
@@ -530,9 +539,10 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
 
     // Staging map of this lane: weight chunks (tiles past the end reread the
     // last tile), activation chunks (padding tokens read token m0), scales.
-    // 32-bit offsets from a workgroup-uniform base: the loads take the
-    // scalar-base form, with no per-lane 64-bit address arithmetic (a TILED
-    // matrix is below 4 GiB: the host checks it).
+    // 32-bit lane offsets into buffer descriptors, the unit's offset in a
+    // scalar register (a TILED matrix is below 4 GiB: the host checks it).
+    // Reads past the activation codes (the last Q8_0 unit past K) return
+    // zeros; their groups have zero scales.
     uint32_t goff[SG::kNW];
     int wdst[SG::kNW];
 #pragma unroll
@@ -558,23 +568,26 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     const bool s_tok_in = s_on && s_tok < Mloc;
     const uint32_t s_row = (uint32_t)(m0 + (s_tok_in ? s_tok : 0)) * (uint32_t)ngroups + 4u * s_h;
 
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(Wm, (uint32_t)ntiles8 * (uint32_t)(p.upr * UB));
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(p.xq, (uint32_t)p.M * (uint32_t)p.K);
+    const uint32_t sbytes = (uint32_t)p.M * (uint32_t)ngroups * 4u;
+    const __amdgpu_buffer_rsrc_t dr = buf_rsrc(p.xd, sbytes), sr = buf_rsrc(p.xs, sbytes);
     v4u rw[SG::kNW], ra[SG::kNA];
     float sd[4];
     uint32_t ss[4] = {0u, 0u, 0u, 0u};
     auto issue = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) rw[n] = *(const v4u *)(Wm + (size_t)u * UB + goff[n]);
+        for (int n = 0; n < SG::kNW; ++n) rw[n] = buf_ld16(wr, goff[n], (uint32_t)u * UB);
 #pragma unroll
-        for (int n = 0; n < SG::kNA; ++n) ra[n] = *(const v4u *)(p.xq + (size_t)u * UE + aoff[n]);
-        const float *xd = p.xd + (size_t)u * G;
+        for (int n = 0; n < SG::kNA; ++n) ra[n] = buf_ld16(xr, aoff[n], (uint32_t)u * UE);
         if constexpr (G == 8) {  // whole units: rows of 8 k groups, 16-byte aligned
-            const float4 d = *(const float4 *)(xd + s_row);
-            sd[0] = d.x;
-            sd[1] = d.y;
-            sd[2] = d.z;
-            sd[3] = d.w;
+            const v4u d = buf_ld16(dr, 4u * s_row, (uint32_t)u * (4 * G));
+            sd[0] = __uint_as_float(d.x);
+            sd[1] = __uint_as_float(d.y);
+            sd[2] = __uint_as_float(d.z);
+            sd[3] = __uint_as_float(d.w);
             if constexpr (T::kAux) {
-                const uint4 v = *(const uint4 *)(p.xs + (size_t)u * G + s_row);
+                const v4u v = buf_ld16(sr, 4u * s_row, (uint32_t)u * (4 * G));
                 ss[0] = v.x;
                 ss[1] = v.y;
                 ss[2] = v.z;
