@@ -174,7 +174,10 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     p.M = M;
     const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(ws[0].ggml_type, p.upr, M) <= kMtLdsBudget;
     if (!few && matmul_mfma_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
-    for (int i = 0; i < n && !few; ++i)  // the MFMA kernel addresses a matrix with 32-bit offsets
+    // The MFMA kernel reads each matrix through a buffer descriptor with a
+    // 32-bit size; the activations (M <= kMaxM rows of K <= kMaxK) stay far
+    // below it.
+    for (int i = 0; i < n && !few; ++i)
         if (tiled_bytes(ws[i].ggml_type, ws[i].row_blocks, ws[i].row_count) >= (1ull << 32)) return M27Q_ERR_SHAPE;
     const ActView a = act_view(xq, M, p.K);
     p.xq = a.q;
