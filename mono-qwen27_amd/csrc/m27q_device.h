@@ -69,9 +69,27 @@ __device__ __forceinline__ float sum8(float v) {
 // roundf(x / d) under fast-math, which compiles to the same multiply by an
 // approximate reciprocal.  Besides d, the two 16-value integer code sums are
 // kept, packed as (int16 lo) | (int16 hi) << 16.
+// roundf(x * id) clamped to +-127.  For |v| < 2^23, (int)(v + copysign(h, v))
+// with h = 0.49999997f (the largest float below 0.5) equals (int)roundf(v):
+// checked over every such float.  Below 0.5 the sum stays below 1; from 0.5
+// on it lands in the right unit interval, ties going away from zero.  The
+// product and the sum are each rounded once, as the host oracle's x * id and
+// roundf are: contracting them into an FMA (the default for HIP) would skip
+// the product's rounding.  |v| stays below 128 here; the clamp handles the
+// saturated conversion of a subnormal scale's 1/d.
 __device__ __forceinline__ int quant_code(float x, float id) {
-    const int t = (int)roundf(x * id);
+#pragma clang fp contract(off)
+    const float v = x * id;
+    const int t = (int)(v + __builtin_copysignf(0.49999997f, v));
     return t > 127 ? 127 : (t < -127 ? -127 : t);
+}
+
+// Four codes in [-127, 127] as the bytes of one word (v_perm_b32 byte picks;
+// selector 0x0c gives a zero byte).
+__device__ __forceinline__ uint32_t pack_codes(int q0, int q1, int q2, int q3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u);
+    return lo | (hi << 16);
 }
 
 __device__ __forceinline__ uint32_t pack_sums(int lo, int hi) {
@@ -116,11 +134,7 @@ __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uin
     const int s_other = dpp_i<kDppXor2>(s);
     *d_out = d;
     *s_out = (threadIdx.x & 2) == 0 ? pack_sums(s, s_other) : pack_sums(s_other, s);
-    const uint32_t w0 = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                        ((uint32_t)q3 << 24);
-    const uint32_t w1 = (uint32_t)(q4 & 0xff) | ((uint32_t)(q5 & 0xff) << 8) | ((uint32_t)(q6 & 0xff) << 16) |
-                        ((uint32_t)q7 << 24);
-    return make_uint2(w0, w1);
+    return make_uint2(pack_codes(q0, q1, q2, q3), pack_codes(q4, q5, q6, q7));
 }
 
 // IQ4_NL / IQ4_XS table (exec:51-55) as bytes: entries 0..3, 4..7, 8..11, 12..15.

@@ -9,7 +9,7 @@ pytestmark = pytest.mark.gpu
 
 def edge_rows(k):
     rng = np.random.default_rng(11)
-    x = rng.standard_normal((6, k)).astype(np.float32)
+    x = rng.standard_normal((7, k)).astype(np.float32)
     x[0, :64] = 0.0                                   # all-zero groups
     x[1, :32] = 127.0 * np.arange(32) / 31.0          # exact multiples of d
     x[1, 32:64] = np.float32(127.0)
@@ -18,14 +18,22 @@ def edge_rows(k):
     x[3] *= np.float32(1e30)                           # huge values
     x[4, ::2] = -x[4, ::2]
     x[5, :32] = -0.0
+    # d = 1 again: values beside the ties and beside 0.5 (the largest float
+    # below 0.5 must give 0, 0.5 itself 1) and subnormal inputs.  (A group
+    # whose amax is below ~3.7e-37 has a subnormal d and an infinite 1/d; the
+    # codes of such a group are outside the defined range of the rule.)
+    x[6, :32] = np.float32(127.0)
+    x[6, 1:16] = np.array([0.49999997, -0.49999997, 0.50000006, -0.50000006, 1.4999999, -1.4999999, 2.4999998,
+                           -2.4999998, 125.49999, -125.49999, 126.50001, -0.0, 1e-40, -1e-40, 3.5],
+                          dtype=np.float32)
     return x
 
 
-@pytest.mark.parametrize("M,K", [(1, 5120), (4, 6144), (16, 17408), (6, 256)])
+@pytest.mark.parametrize("M,K", [(1, 5120), (4, 6144), (16, 17408), (7, 256)])
 def test_quant_act_bitexact(m27q, ora, dev, M, K):
     rng = np.random.default_rng(M * 1000 + K)
     x = (rng.standard_normal((M, K)) * 10.0 ** rng.integers(-3, 4, (M, 1))).astype(np.float32)
-    if M == 6:
+    if M == 7:
         x = edge_rows(K)
     say("quant_act", M, K)
     act = m27q.Act(M, K, dev)

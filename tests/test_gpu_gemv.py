@@ -251,17 +251,21 @@ def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     rb = k // m27q.BLOCK_ELEMS[t]
     wb = weights(ora, type_name, rc, k, 10)
     w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
-    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
-    xd = to_dev(x, dev)
+    from test_gpu_act import edge_rows
     res = to_dev(np.random.default_rng(2).standard_normal(rc).astype(np.float32), dev)
-    y0 = torch.empty(rc, dtype=torch.float32, device=dev)
-    y1 = torch.empty(rc, dtype=torch.float32, device=dev)
-    say("matvec fp32 input", type_name)
-    m27q.matvec(w, xd, y0, residual=res)
-    act = m27q.Act(1, k, dev)
-    m27q.quant_act(xd, act)
-    m27q.matvec_q8(w, act, y1, residual=res)
-    assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32))
+    # random x, then the quantizer's edge rows (ties, values beside 0.5,
+    # subnormal scales) laid end to end
+    for xi, x in enumerate((np.random.default_rng(1).standard_normal(k).astype(np.float32),
+                            np.resize(edge_rows(256).reshape(-1), k).astype(np.float32))):
+        xd = to_dev(x, dev)
+        y0 = torch.empty(rc, dtype=torch.float32, device=dev)
+        y1 = torch.empty(rc, dtype=torch.float32, device=dev)
+        say("matvec fp32 input", type_name, xi)
+        m27q.matvec(w, xd, y0, residual=res)
+        act = m27q.Act(1, k, dev)
+        m27q.quant_act(xd, act)
+        m27q.matvec_q8(w, act, y1, residual=res)
+        assert np.array_equal(to_host(y0).view(np.uint32), to_host(y1).view(np.uint32)), xi
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q4_K", 6144, 5120), ("Q8_0", 13, 160), ("Q4_K", 40, 512),
