@@ -84,6 +84,19 @@ __device__ __forceinline__ int quant_code(float x, float id) {
     return t > 127 ? 127 : (t < -127 ? -127 : t);
 }
 
+// amax / 127, correctly rounded, in three operations: q = amax * rn(1/127),
+// then one FMA correction from the exact residual amax - 127 q.  Equal to the
+// IEEE division for every non-negative finite float, subnormals included
+// (checked over all of them; the kernels keep fp32 denormals); +inf is
+// passed through as the division would.
+__device__ __forceinline__ float div127(float a) {
+#pragma clang fp contract(off)
+    const float c = 1.0f / 127.0f;
+    const float q = a * c;
+    const float d = __builtin_fmaf(__builtin_fmaf(-q, 127.0f, a), c, q);
+    return a == __builtin_inff() ? a : d;
+}
+
 // Four codes in [-127, 127] as the bytes of one word (v_perm_b32 byte picks;
 // selector 0x0c gives a zero byte).
 __device__ __forceinline__ uint32_t pack_codes(int q0, int q1, int q2, int q3) {
@@ -102,7 +115,7 @@ __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
     float amax = fabsf(v);
 #pragma unroll
     for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    const float d = amax / 127.0f;
+    const float d = div127(amax);
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q = quant_code(v, id);
     int s = q;
@@ -125,7 +138,7 @@ __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uin
                        fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
     amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
     amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
-    const float d = amax / 127.0f;
+    const float d = div127(amax);
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q0 = quant_code(a.x, id), q1 = quant_code(a.y, id), q2 = quant_code(a.z, id), q3 = quant_code(a.w, id);
     const int q4 = quant_code(b.x, id), q5 = quant_code(b.y, id), q6 = quant_code(b.z, id), q7 = quant_code(b.w, id);
