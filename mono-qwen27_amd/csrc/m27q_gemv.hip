@@ -42,8 +42,8 @@
 namespace m27q {
 
 // Activation staging into LDS: codes[Kp] | d[Kp/32] | aux[Kp/32] (zero
-// padded from K to Kp).  stage_issue() loads the first batch into registers;
-// stage_finish() converts and stores it, then handles any further batches.
+// padded from K to Kp).  stage_load() loads one batch into registers (the
+// first before the first weight loads), stage_store() converts and stores it.
 constexpr int kStageSlots = 4;  // per thread: 4 x 32 B of fp32 values, or 4 x 16 B of codes
 
 template <bool XF32>
