@@ -45,12 +45,17 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     act16 = m27q.Act(16, 5120, dev)
     X16 = torch.empty((16, 5120), dtype=torch.float32, device=dev)
     Y16 = torch.empty((16, 2048), dtype=torch.float32, device=dev)
+    act5 = m27q.Act(5, 5120, dev)
+    X5 = torch.empty((5, 5120), dtype=torch.float32, device=dev)
+    Y5 = torch.empty((5, 8192), dtype=torch.float32, device=dev)      # two row sets per tile
+    Y5q = torch.empty((5, 1024), dtype=torch.float32, device=dev)
+    Y5g = torch.empty((5, 2048), dtype=torch.float32, device=dev)
     logits = torch.empty(8192, dtype=torch.float32, device=dev)
     scratch = torch.empty(m27q.topk_scratch_bytes(8192, k), dtype=torch.uint8, device=dev)
     idx = torch.empty(k, dtype=torch.int32, device=dev)
     val = torch.empty(k, dtype=torch.float32, device=dev)
     tok = torch.empty(1, dtype=torch.int32, device=dev)
-    outs = [x, qv, h, f, fq.buf, out, Y2, Y16, logits, idx, val, tok]
+    outs = [x, qv, h, f, fq.buf, out, Y2, Y16, Y5, Y5q, Y5g, logits, idx, val, tok]
 
     def step(s):
         m27q.embed_rows(W["emb"], ids, x, bad, stream=s)
@@ -62,6 +67,9 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
         m27q.matmul_q8(W["q"], act2, Y2, stream=s)
         m27q.quant_act(X16, act16, stream=s)
         m27q.matmul_q8(W["gate"], act16, Y16, stream=s)
+        m27q.quant_act(X5, act5, stream=s)
+        m27q.matmul_q8(W["lm"], act5, Y5, stream=s)
+        m27q.matmul_q8_multi([W["q"], W["gate"]], act5, [Y5q, Y5g], stream=s)
         m27q.matvec(W["lm"], out, logits, stream=s)
         m27q.topk(logits, k, idx, val, scratch, stream=s)
         m27q.sample(idx, val, k, 0.8, 0.05, 0.95, u, tok, stream=s)
@@ -72,17 +80,18 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
         ids.copy_(torch.from_numpy(np.array([7 + 13 * i, 4000 - 5 * i], np.int32)))
         u.fill_(0.15 + 0.3 * i)
         X16.copy_(torch.from_numpy(rng.standard_normal((16, 5120)).astype(np.float32)))
+        X5.copy_(torch.from_numpy(rng.standard_normal((5, 5120)).astype(np.float32)))
         torch.cuda.synchronize()
 
     # eager reference results for three input sets
     want = []
     for i in range(3):
         set_inputs(i)
-        X16_i = X16.clone()
+        X16_i, X5_i = X16.clone(), X5.clone()
         say("graph eager", i)
         step(torch.cuda.current_stream())
         torch.cuda.synchronize()
-        want.append(([bits(t) for t in outs], X16_i))
+        want.append(([bits(t) for t in outs], X16_i, X5_i))
     assert to_host(bad)[0] == 0
 
     s = torch.cuda.Stream()
@@ -99,6 +108,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
         for i in range(3):
             set_inputs(i)
             X16.copy_(want[i][1])
+            X5.copy_(want[i][2])
             for t in outs:
                 t.zero_()
             torch.cuda.synchronize()
