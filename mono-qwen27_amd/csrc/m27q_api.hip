@@ -172,8 +172,8 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
     p.K = k_of(&ws[0]);
     p.M = M;
-    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(ws[0].ggml_type, p.upr, M) <= kMtLdsBudget;
-    if (!few && matmul_mfma_lds_bytes(ws[0].ggml_type, p.upr) > lds_limit()) return M27Q_ERR_SHAPE;
+    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(ws[0].ggml_type, p.upr) <= kMtLdsBudget;
+    if (!few && matmul_mfma_lds_bytes(ws[0].ggml_type) > lds_limit()) return M27Q_ERR_SHAPE;
     // The MFMA kernel reads each matrix through a buffer descriptor with a
     // 32-bit size; the activations (M <= kMaxM rows of K <= kMaxK) stay far
     // below it.

@@ -196,7 +196,7 @@ static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
     }
 }
 
-size_t matmul_mt_lds_bytes(uint32_t type, int upr, int) {
+size_t matmul_mt_lds_bytes(uint32_t type, int upr) {
     // the largest over the launch shapes the selection can return
     auto one = [&](auto tag) -> size_t {
         using T = decltype(tag);

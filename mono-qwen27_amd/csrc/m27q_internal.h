@@ -91,12 +91,13 @@ struct MatmulMultiParams {
     const uint32_t *xs;
 };
 hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s);
+// Few-token products on the GEMV streaming structure (m27q_gemv_mt.hip): two
+// activation rows, TILED weights.
+size_t matmul_mt_lds_bytes(uint32_t type, int upr);
+hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
 // int8-MFMA small-M products (m27q_mma.hip): TILED weights, any M (16 tokens
 // per launch).
-// Few-token products on the GEMV streaming structure (m27q_gemv_mt.hip).
-size_t matmul_mt_lds_bytes(uint32_t type, int upr, int M);
-hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
-size_t matmul_mfma_lds_bytes(uint32_t type, int upr);
+size_t matmul_mfma_lds_bytes(uint32_t type);
 hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
 
 }  // namespace m27q

@@ -691,13 +691,13 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
 }
 
 template <class T, int PK, int KS>
-static size_t mfma_lds(int) {
+static size_t mfma_lds() {
     return (size_t)KS * Stage<T, PK>::kBytes;
 }
 
 template <class T, int PK, int KS>
 static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
-    const size_t lds = mfma_lds<T, PK, KS>(p.upr);
+    const size_t lds = mfma_lds<T, PK, KS>();
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
         p.wg_start[i] = total;
@@ -748,11 +748,12 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
 
 template <class T>
 static size_t mfma_lds_max() {
-    return std::max(mfma_lds<T, 1, 8>(0), mfma_lds<T, 2, 8>(0));
+    return std::max(mfma_lds<T, 1, 8>(), mfma_lds<T, 2, 8>());
 }
 
-size_t matmul_mfma_lds_bytes(uint32_t type, int) {
-    // the largest over the shapes the selection can return (KS = 8)
+size_t matmul_mfma_lds_bytes(uint32_t type) {
+    // the largest over the shapes the selection can return (KS = 8); the
+    // staging is per unit, so it does not depend on K
     switch (type) {
         case kQ4_K: return mfma_lds_max<MmQ4K>();
         case kQ5_K: return mfma_lds_max<MmQ5K>();
