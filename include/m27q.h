@@ -180,8 +180,10 @@ M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const vo
                                           hipStream_t stream);
 
 /* y[r] = silu(Wg x)[r] * (Wu x)[r]; gate and up of one type, layout and shape;
- * yq may be NULL.  Replaces l_ffn_gate_up_swiglu / k_q4k_q4k_swiglu_dp4a
- * (exec:2239-2261, :369-417), which takes fp32 x. */
+ * yq may be NULL (where it is not, y is quantized into it by a second launch
+ * on the same stream, with the codes of m27q_quant_act).  Replaces
+ * l_ffn_gate_up_swiglu / k_q4k_q4k_swiglu_dp4a (exec:2239-2261, :369-417),
+ * which takes fp32 x. */
 M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const float *x, float *y,
                                      void *yq, hipStream_t stream);
 M27Q_API m27q_status m27q_ffn_swiglu_q8(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,

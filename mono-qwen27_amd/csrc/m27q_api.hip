@@ -114,7 +114,14 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     long long rows_total = 0;
     for (int i = 0; i < n; ++i) rows_total += ws[i].row_count;
     if (swiglu) rows_total = ws[0].row_count;
-    const int cfg = pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq != nullptr, rows_total, p.upr);
+    // A SwiGLU product quantizes its output in a second launch (the quantizer
+    // of m27q_quant_act, same codes): its 8-row workgroups spread evenly over
+    // the CUs (2176 for gate/up, 8.5 per CU), where quantizing in the product
+    // needs whole 32-row groups per workgroup (544, 2 or 3 per CU, and a launch
+    // ends with its most loaded CUs).  Measured 0.9 us faster per layer.
+    const bool quant_after = yq && swiglu;
+    const int cfg = pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,
+                                  rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
     if (x) {
         p.x = x;
@@ -137,13 +144,16 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     else p.res[0] = residual;
     p.wg_start[nout] = total;
     p.nmat = nout;
-    if (yq) {
-        const ActView a = act_view(yq, 1, (int)ws[0].row_count);
-        p.oq = (int8_t *)a.q;
-        p.od = (float *)a.d;
-        p.os = (uint32_t *)a.s;
+    const ActView ya = yq ? act_view(yq, 1, (int)ws[0].row_count) : ActView{};
+    if (yq && !quant_after) {
+        p.oq = (int8_t *)ya.q;
+        p.od = (float *)ya.d;
+        p.os = (uint32_t *)ya.s;
     }
-    return hip_status(launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, swiglu, cfg, p, stream));
+    hipError_t e = launch_gemv_q8(ws[0].ggml_type, (int)ws[0].layout, swiglu, cfg, p, stream);
+    if (e == hipSuccess && quant_after)
+        e = launch_quant_act(ys[0], nullptr, ws[0].row_count, (int8_t *)ya.q, (float *)ya.d, (uint32_t *)ya.s, stream);
+    return hip_status(e);
 }
 
 // Small-M products for TILED weights: up to kMtMaxM tokens on the GEMV
@@ -212,7 +222,7 @@ M27Q_API size_t m27q_act_bytes(int M, int K) {
 static m27q_status quant_act_impl(const float *x, const float *gate, int M, int K, void *xq, hipStream_t s) {
     if (!x || !xq) return M27Q_ERR_NULL;
     if (M <= 0 || M > 1 << 16 || K < 32 || K % 32 || K > kMaxK) return M27Q_ERR_SHAPE;
-    if (!aligned(xq, 16) || !aligned(x, 4)) return M27Q_ERR_LAYOUT;
+    if (!aligned(xq, 16) || !aligned(x, 4) || (gate && !aligned(gate, 4))) return M27Q_ERR_LAYOUT;
     const ActView a = act_view(xq, M, K);
     return hip_status(launch_quant_act(x, gate, (long long)M * K, (int8_t *)a.q, (float *)a.d, (uint32_t *)a.s, s));
 }

@@ -11,6 +11,10 @@ namespace m27q {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
+// x * sigmoid(g), the gated activation of k_quant_q8_1_fused_gate
+// (exec:109-138); the one definition both quantizer kernels use.
+__device__ __forceinline__ float gated(float x, float g) { return x * (1.0f / (1.0f + expf(-g))); }
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     const uint16_t b = (uint16_t)bits16;
     _Float16 h;

@@ -27,8 +27,11 @@
 // (shapes written (KS, TPW) have WT = TPW).  Small products need more waves
 // per row than their row count provides: 2048 rows are 256 tiles, one per CU.
 //
-// Products that quantize their output (yq) need whole 32-row groups per
-// workgroup (TPW >= 4) and use CfgQ.  GGUF-layout weights (the compatibility
+// Products that quantize their output (yq) in the kernel need whole 32-row
+// groups per workgroup (TPW >= 4) and use CfgQ; SwiGLU products instead take
+// their own shape and leave the quantization to a second launch (544 32-row
+// workgroups put 3 on 32 of the 256 CUs, and a launch ends with its most
+// loaded CUs: (4,1) + the quantizer 23.05 us against 23.93 in one launch).  GGUF-layout weights (the compatibility
 // path) follow the same rules: q/k/v 7.97 us and o 7.83 with them against 8.66
 // and 8.20 on (4,1) alone; gate/up and down pay for the row-major blocks
 // (30.6 and 21.6 us against 24.2 and 16.4 TILED).  Each shape can be
