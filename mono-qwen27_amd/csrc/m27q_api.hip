@@ -14,6 +14,9 @@ namespace {
 
 constexpr size_t kActAlign = 256;
 constexpr int kMaxK = 1 << 20;
+#ifndef M27Q_BALANCE
+#define M27Q_BALANCE 1
+#endif
 constexpr int kMaxM = 64;
 constexpr int kMaxTopK = 64;
 
@@ -22,6 +25,20 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 // LDS limit of one workgroup on the current device (160 KiB on gfx950).
+// Compute units of the current device (256 on MI355X), for balanced tiling.
+int cu_count() {
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cached = v;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
 size_t lds_limit() {
     static size_t cached = 0;
     if (!cached) {
@@ -120,8 +137,19 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     // needs whole 32-row groups per workgroup (544, 2 or 3 per CU, and a launch
     // ends with its most loaded CUs).  Measured 0.9 us faster per layer.
     const bool quant_after = yq && swiglu;
-    const int cfg = pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,
-                                  rows_total, p.upr);
+    // A single product on a quantized activation with between 2 and TPW
+    // tiles per CU (down: 640 tiles on 256 CUs) spreads its tiles evenly over
+    // one workgroup per CU: one tile per workgroup puts 3 on half the CUs and 2
+    // on the rest, and a launch ends with its most loaded CUs (down 15.9 us
+    // against 16.45).  On an fp32 activation each workgroup also quantizes x,
+    // and o measured 0.2 us slower this way.
+    const long long tiles0 = tiles_of(ws[0].row_count);
+    const int cus = cu_count();
+    const bool bal = M27Q_BALANCE && n == 1 && !swiglu && !yq && !x && tiles0 > 2LL * cus &&
+                     tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB) * cus;
+    const int cfg = bal ? kCfgB
+                        : pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,
+                                        rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
     if (x) {
         p.x = x;
@@ -138,8 +166,9 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
         p.y[i] = ys[i];
         p.rc[i] = (int)ws[i].row_count;
         p.wg_start[i] = total;
-        total += (tiles_of(ws[i].row_count) + tpw - 1) / tpw;
+        total += bal ? cus : (tiles_of(ws[i].row_count) + tpw - 1) / tpw;
     }
+    p.bal = bal ? 1 : 0;
     if (swiglu) p.W[1] = (const uint8_t *)ws[1].ptr;
     else p.res[0] = residual;
     p.wg_start[nout] = total;

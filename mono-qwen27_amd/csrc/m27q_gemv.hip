@@ -173,8 +173,17 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     for (int k = 1; k < kMaxMulti; ++k)
         if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) m = k;
     const int rc = p.rc[m];
-    const int tile0 = ((int)blockIdx.x - p.wg_start[m]) * TPW;
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
+    // Tiles of this workgroup: TPW from tile0, or, with balanced tiling, nt
+    // of them (TPW - 1 or TPW); the slots past nt reread the workgroup's last
+    // tile (cache hits) and their rows are not written.
+    const int wg = (int)blockIdx.x - p.wg_start[m];
+    int tile0 = wg * TPW, nt = TPW;
+    if (p.bal) {
+        const int G = p.wg_start[m + 1] - p.wg_start[m];
+        tile0 = (int)((long long)wg * ntiles / G);
+        nt = (int)((long long)(wg + 1) * ntiles / G) - tile0;
+    }
 
     // K slice of this wave: units [ub, ub + nu); a wave with no units reads a
     // valid unit and discards it.
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     const uint8_t *W[NM];
     W[0] = p.W[m];
     if constexpr (SWIGLU) W[NM - 1] = p.W[1];
-    const UnitStream<T, LAYOUT, NM, WT> ws(W, tile0 + tg * WT, ntiles, rc, p.rb, p.upr, lane);
+    const UnitStream<T, LAYOUT, NM, WT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, p.rb, p.upr, lane);
     typename T::Frag fa[NM][WT], fb[NM][WT];
     ws.load(fa, min(ub, p.upr - 1));
 
@@ -242,15 +251,16 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
         v = red[t];
 #pragma unroll
         for (int w = 1; w < KS; ++w) v += red[w * NR + t];
+        const bool own = row < rc && t < nt * kTileRows;
         if constexpr (SWIGLU) {
             float vu = red[KS * NR + t];
 #pragma unroll
             for (int w = 1; w < KS; ++w) vu += red[(KS + w) * NR + t];
             v = silu(v) * vu;
         } else {
-            if (p.res[m] && row < rc) v += p.res[m][row];
+            if (p.res[m] && own) v += p.res[m][row];
         }
-        if (row < rc) p.y[m][row] = v;
+        if (own) p.y[m][row] = v;
     }
     if constexpr (NR % 32 == 0)
         if (p.oq) quant_output<NR>(p, tile0 * kTileRows, rc, v);
@@ -396,6 +406,9 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
                        // other instantiation keeps the tiles per workgroup the grid was sized for
             if constexpr (!SWIGLU && XF32) return launch_q8_cfg<T, LAYOUT, Cfg822, SWIGLU, XF32>(p, s);
             return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
+        case kCfgB:  // balanced tiling, single products without the SwiGLU epilogue only
+            if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, CfgB, SWIGLU, XF32>(p, s);
+            return hipErrorInvalidValue;
         default: return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     }
 }
@@ -427,6 +440,7 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
         case kCfgQ: return lds_sw<T, CfgQ>(upr, swiglu);
         case kCfg161: return swiglu ? lds_sw<T, Cfg41>(upr, swiglu) : lds_sw<T, Cfg161>(upr, swiglu);
         case kCfg822: return std::max(lds_sw<T, Cfg42>(upr, swiglu), lds_sw<T, Cfg822>(upr, swiglu));
+        case kCfgB: return lds_sw<T, CfgB>(upr, swiglu);
         default: return lds_sw<T, Cfg41>(upr, swiglu);
     }
 }
@@ -450,6 +464,7 @@ int gemv_q8_tiles_per_wg(int cfg) {
         case kCfgQ: return CfgQ::TPW;
         case kCfg161: return Cfg161::TPW;
         case kCfg822: return Cfg822::TPW;
+        case kCfgB: return CfgB::TPW;
         default: return Cfg41::TPW;
     }
 }

@@ -68,6 +68,9 @@ struct GemvCfg {
 #ifndef M27Q_CFG_822
 #define M27Q_CFG_822 8, 2, 2
 #endif
+#ifndef M27Q_CFG_B
+#define M27Q_CFG_B 4, 3, 1
+#endif
 
 using Cfg41 = GemvCfg<M27Q_CFG_41>;
 using Cfg81 = GemvCfg<M27Q_CFG_81>;
@@ -76,10 +79,11 @@ using Cfg84 = GemvCfg<M27Q_CFG_84>;
 using CfgQ = GemvCfg<M27Q_CFG_Q>;
 using Cfg161 = GemvCfg<M27Q_CFG_161>;
 using Cfg822 = GemvCfg<M27Q_CFG_822>;
+using CfgB = GemvCfg<M27Q_CFG_B>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
 static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 
-enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6 };
+enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) over upr units per row.

@@ -30,6 +30,9 @@ struct GemvParams {
     const uint32_t *xs;
     // ... or fp32 activation
     const float *x;
+    // balanced tiling: workgroup w of matrix m (G workgroups, T tiles) owns
+    // tiles [w T / G, (w + 1) T / G), at most C::TPW of them
+    int bal;
     // optional fused quantization of the output vector
     int8_t *oq;
     float *od;

@@ -240,12 +240,15 @@ def test_matvec_dense(m27q, ora, dev, type_name):
     assert (np.abs(to_host(y) - want) <= 1e-5 * scale).all()
 
 
-@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 5120, 6144), ("Q4_K", 17408, 5120),
-                                             ("Q8_0", 2048, 6144), ("Q5_K", 5120, 6144), ("IQ4_XS", 5120, 6144)])
+@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 5120, 17408), ("Q4_K", 4096, 6144), ("Q4_K", 17408, 5120),
+                                             ("Q8_0", 2048, 6144), ("Q5_K", 4096, 6144), ("IQ4_XS", 4096, 6144)])
 def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so at
-    shapes where both input forms launch the same workgroup shape the product
-    is bit-identical to quant_act followed by the quantized-input product."""
+    shapes where both input forms split K alike the product is bit-identical to
+    quant_act followed by the quantized-input product.  (The down shape: the
+    quantized form's balanced tiling and the fp32 form's one tile per
+    workgroup both split K four ways; at 5120 x 6144 the two forms split it
+    four and eight ways, so 4096 rows stand in there.)"""
     import torch
     t = getattr(m27q, type_name)
     rb = k // m27q.BLOCK_ELEMS[t]
