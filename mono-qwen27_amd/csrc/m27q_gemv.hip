@@ -21,6 +21,9 @@
 //   issued before the first weight loads.
 //   Epilogues: + residual, SwiGLU of two matrices (silu(gate) * up), and the
 //   per-32 quantization of the output rows for the next product.
+//   Balanced tiling (GemvParams::bal): workgroup w of G owns tiles
+//   [w T / G, (w + 1) T / G), so one workgroup per CU carries an even share
+//   of a matrix whose tile count is not a multiple of the CU count.
 //
 // fp32-activation products (exact dequantization, fp32 accumulation) keep the
 // simpler one-wave-per-tile mapping: they are the fallback, not the hot path.

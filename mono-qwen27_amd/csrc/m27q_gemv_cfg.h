@@ -24,14 +24,23 @@
 //   Q8_0 2048 x 2048 (draft)                 (16,1) 3.43 us, (8,1) 3.70, (8,4) 4.32
 //   Q8_0 6144 x 2048 (draft)                 (8,1)  4.83 us, (8,4) 5.12, (16,1) 6.78
 //   Q8_0 2048 x 6144 (draft)                 (16,1) 5.26 us, (8,1) 5.78, (4,1) 6.80
-// (shapes written (KS, TPW) have WT = TPW).  Small products need more waves
-// per row than their row count provides: 2048 rows are 256 tiles, one per CU.
+// (shapes written (KS, TPW) have WT = TPW; figures from when they were
+// chosen, before the cheaper activation quantizer).  Small products need more
+// waves per row than their row count provides: 2048 rows are 256 tiles, one
+// per CU.
 //
-// Products that quantize their output (yq) in the kernel need whole 32-row
-// groups per workgroup (TPW >= 4) and use CfgQ; SwiGLU products instead take
-// their own shape and leave the quantization to a second launch (544 32-row
-// workgroups put 3 on 32 of the 256 CUs, and a launch ends with its most
-// loaded CUs: (4,1) + the quantizer 23.05 us against 23.93 in one launch).  GGUF-layout weights (the compatibility
+// A launch ends with its most loaded CUs (the memory system shares bandwidth
+// roughly per CU), so how evenly the workgroups spread over the 256 CUs
+// matters as much as their shape:
+//   - products that quantize their output (yq) in the kernel need whole 32-row
+//     groups per workgroup (TPW >= 4) and use CfgQ; SwiGLU products instead
+//     take their own shape and leave the quantization to a second launch (544
+//     32-row workgroups put 3 on 32 CUs: (4,1) + the quantizer 23.05 us
+//     against 23.93 in one launch);
+//   - a single product on a quantized x with 2 to 3 tiles per CU (down, 640
+//     tiles) takes CfgB with balanced tiling, one workgroup per CU (15.8 us
+//     against 16.45 with one tile per workgroup).
+// GGUF-layout weights (the compatibility
 // path) follow the same rules: q/k/v 7.97 us and o 7.83 with them against 8.66
 // and 8.20 on (4,1) alone; gate/up and down pay for the row-major blocks
 // (30.6 and 21.6 us against 24.2 and 16.4 TILED).  Each shape can be
