@@ -137,15 +137,16 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     // needs whole 32-row groups per workgroup (544, 2 or 3 per CU, and a launch
     // ends with its most loaded CUs).  Measured 0.9 us faster per layer.
     const bool quant_after = yq && swiglu;
-    // A single product on a quantized activation with between 2 and TPW
-    // tiles per CU (down: 640 tiles on 256 CUs) spreads its tiles evenly over
-    // one workgroup per CU: one tile per workgroup puts 3 on half the CUs and 2
-    // on the rest, and a launch ends with its most loaded CUs (down 15.9 us
-    // against 16.45).  On an fp32 activation each workgroup also quantizes x,
-    // and o measured 0.2 us slower this way.
+    // A single product with between 2 and TPW tiles per CU (down: 640 tiles
+    // on 256 CUs) spreads its tiles evenly over one workgroup per CU: one tile
+    // per workgroup puts 3 on half the CUs and 2 on the rest, and a launch ends
+    // with its most loaded CUs (down on int8 codes 15.9 us against 16.45, on
+    // fp32 x 17.3 us against 19.7).  On an fp32 activation each workgroup also
+    // quantizes x, which on short rows costs more than the balance gains (o,
+    // 6144 columns: 0.2 us slower), so fp32 input balances from 10240 columns.
     const long long tiles0 = tiles_of(ws[0].row_count);
     const int cus = cu_count();
-    const bool bal = M27Q_BALANCE && n == 1 && !swiglu && !yq && !x && tiles0 > 2LL * cus &&
+    const bool bal = M27Q_BALANCE && n == 1 && !swiglu && !yq && (!x || p.K >= 10240) && tiles0 > 2LL * cus &&
                      tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB) * cus;
     const int cfg = bal ? kCfgB
                         : pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,

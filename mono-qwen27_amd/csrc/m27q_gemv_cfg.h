@@ -37,9 +37,11 @@
 //     take their own shape and leave the quantization to a second launch (544
 //     32-row workgroups put 3 on 32 CUs: (4,1) + the quantizer 23.05 us
 //     against 23.93 in one launch);
-//   - a single product on a quantized x with 2 to 3 tiles per CU (down, 640
-//     tiles) takes CfgB with balanced tiling, one workgroup per CU (15.8 us
-//     against 16.45 with one tile per workgroup).
+//   - a single product with 2 to 3 tiles per CU (down, 640 tiles) takes CfgB
+//     with balanced tiling, one workgroup per CU (on a quantized x 15.8 us
+//     against 16.45 with one tile per workgroup; on an fp32 x, quantized by
+//     every workgroup, 17.3 us against 19.7, but only on rows of 10240
+//     columns or more: o's 6144 measured slower).
 // GGUF-layout weights (the compatibility
 // path) follow the same rules: q/k/v 7.97 us and o 7.83 with them against 8.66
 // and 8.20 on (4,1) alone; gate/up and down pay for the row-major blocks

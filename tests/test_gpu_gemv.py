@@ -245,10 +245,9 @@ def test_matvec_dense(m27q, ora, dev, type_name):
 def test_fp32_input_equals_two_step(m27q, ora, dev, type_name, rc, k):
     """In-kernel quantization of fp32 x gives the codes of m27q_quant_act, so at
     shapes where both input forms split K alike the product is bit-identical to
-    quant_act followed by the quantized-input product.  (The down shape: the
-    quantized form's balanced tiling and the fp32 form's one tile per
-    workgroup both split K four ways; at 5120 x 6144 the two forms split it
-    four and eight ways, so 4096 rows stand in there.)"""
+    quant_act followed by the quantized-input product.  (The down shape: both
+    forms take balanced tiling and split K four ways; at 5120 x 6144 the two
+    forms split it four and eight ways, so 4096 rows stand in there.)"""
     import torch
     t = getattr(m27q, type_name)
     rb = k // m27q.BLOCK_ELEMS[t]
