@@ -289,6 +289,36 @@ def test_fp32_input_vs_oracle(m27q, ora, dev, type_name, rc, k):
     assert (np.abs(to_host(y) - want) <= int_dot_tol(nrm)).all()
 
 
+@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 4100, 10240), ("Q4_K", 6141, 10240)])
+def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k):
+    """Balanced tiling at the ends of its range on 256 CUs: 513 tiles (one
+    workgroup with 3, the rest with 2, which reread their last tile) and 768
+    (3 each), both with a ragged last tile.  The quantized-input product
+    against the integer-dot oracle; the fp32-input product (balanced too from
+    10240 columns) bit-identical to it; the rows past row_count untouched."""
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 12)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    x = np.random.default_rng(13).standard_normal(k).astype(np.float32)
+    xd = to_dev(x, dev)
+    act = m27q.Act(1, k, dev)
+    m27q.quant_act(xd, act)
+    guard = np.float32(-7.25)
+    y0 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
+    y1 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
+    say("balanced tiling", type_name, rc, k)
+    m27q.matvec_q8(w, act, y1[:rc])
+    q, d, s = ora.quant_act(x)
+    want, nrm = ora.gemv_act(t, wb, rb, rc, q, d, s)
+    got = to_host(y1)
+    assert (np.abs(got[:rc] - want) <= int_dot_tol(nrm)).all()
+    assert (got[rc:] == guard).all()
+    m27q.matvec(w, xd, y0[:rc])
+    assert np.array_equal(to_host(y0).view(np.uint32), got.view(np.uint32))
+
+
 def test_fp32_input_multi_and_swiglu(m27q, ora, dev):
     import torch
     k = 5120
