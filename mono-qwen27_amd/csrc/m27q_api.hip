@@ -3,6 +3,7 @@
 // Every check runs on the host before the first HIP call, so a bad argument
 // returns a status without touching the device (the reference's launchers
 // return silently instead, exec:2034, :2056-2059).
+#include <atomic>
 #include <climits>
 #include <cmath>
 
@@ -24,37 +25,39 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// LDS limit of one workgroup on the current device (160 KiB on gfx950).
-// Compute units of the current device (256 on MI355X), for balanced tiling.
-int cu_count() {
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            cached = v;
-        else
-            cached = 256;
+// An attribute of the current device, cached per device (a partitioned
+// MI355X shows fewer CUs per device, and a process may drive several).
+// Concurrent first calls may both query; they store the same value.
+constexpr int kMaxDevices = 64;
+int device_attr(hipDeviceAttribute_t a, std::atomic<int> (&cache)[kMaxDevices], int fallback) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return fallback;
+    if (dev < kMaxDevices) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
     }
-    return cached;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, a, dev) != hipSuccess || v <= 0) return fallback;
+    if (dev < kMaxDevices) cache[dev].store(v, std::memory_order_relaxed);
+    return v;
 }
 
+// Compute units of the current device (256 on MI355X), for balanced tiling.
+int cu_count() {
+    static std::atomic<int> cache[kMaxDevices];
+    return device_attr(hipDeviceAttributeMultiprocessorCount, cache, 256);
+}
+
+// LDS limit of one workgroup on the current device (160 KiB on gfx950).
 size_t lds_limit() {
-    static size_t cached = 0;
-    if (!cached) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
-            cached = (size_t)v;
-        else
-            cached = 64 * 1024;
-    }
-    return cached;
+    static std::atomic<int> cache[kMaxDevices];
+    return (size_t)device_attr(hipDeviceAttributeMaxSharedMemoryPerBlock, cache, 64 * 1024);
 }
 
 int k_of(const m27q_weight *w) { return (int)w->row_blocks * block_elems(w->ggml_type); }
 
-// Shared weight checks.  quant_only: Q4_K / Q6_K / Q8_0 only.
+// Shared weight checks.  quant_only: the integer-dot types (Q4_K, Q5_K,
+// Q6_K, Q8_0, IQ4_XS), not F16 / F32.
 m27q_status check_weight(const m27q_weight *w, bool quant_only) {
     if (!w || !w->ptr) return M27Q_ERR_NULL;
     const uint32_t t = w->ggml_type;
