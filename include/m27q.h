@@ -71,8 +71,9 @@ enum { M27Q_LAYOUT_GGUF = 0, M27Q_LAYOUT_TILED = 1 };
 typedef struct m27q_weight {
     const void *ptr;        /* device pointer (16-byte aligned for TILED) */
     uint32_t ggml_type;     /* M27Q_TYPE_* */
-    uint32_t row_blocks;    /* blocks per row (K / block size; K for F16/F32) */
-    uint32_t row_count;     /* rows (N) */
+    uint32_t row_blocks;    /* blocks per row (K / block size; K for F16/F32);
+                               K <= 2^20 */
+    uint32_t row_count;     /* rows (N), 1 .. 2^24 */
     uint32_t layout;        /* M27Q_LAYOUT_* */
 } m27q_weight;
 

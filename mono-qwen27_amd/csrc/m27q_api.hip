@@ -4,7 +4,6 @@
 // returns a status without touching the device (the reference's launchers
 // return silently instead, exec:2034, :2056-2059).
 #include <atomic>
-#include <climits>
 #include <cmath>
 
 #include "m27q_internal.h"
@@ -15,6 +14,9 @@ namespace {
 
 constexpr size_t kActAlign = 256;
 constexpr int kMaxK = 1 << 20;
+// Rows per weight: one-tile workgroups of up to 1024 threads keep every grid
+// below 2^32 work-items (the dispatch packet's limit).
+constexpr uint32_t kMaxRows = 1u << 24;
 #ifndef M27Q_BALANCE
 #define M27Q_BALANCE 1
 #endif
@@ -63,7 +65,7 @@ m27q_status check_weight(const m27q_weight *w, bool quant_only) {
     const uint32_t t = w->ggml_type;
     if (!block_elems(t)) return M27Q_ERR_TYPE;
     if (quant_only && !is_quant(t)) return M27Q_ERR_TYPE;
-    if (w->row_blocks == 0 || w->row_count == 0 || w->row_count > (uint32_t)INT_MAX / 2) return M27Q_ERR_SHAPE;
+    if (w->row_blocks == 0 || w->row_count == 0 || w->row_count > kMaxRows) return M27Q_ERR_SHAPE;
     if ((long long)w->row_blocks * block_elems(t) > kMaxK) return M27Q_ERR_SHAPE;
     if (w->layout == M27Q_LAYOUT_TILED) {
         if (!is_quant(t)) return M27Q_ERR_LAYOUT;

@@ -122,6 +122,8 @@ def test_validation_matvec_q8(m27q):
     assert L.m27q_matvec_q8(C.byref(W(m27q, t=m27q.F16, layout=m27q.GGUF)), FAKE, FAKE, None, None, None) == 3
     assert L.m27q_matvec_q8(C.byref(W(m27q, rb=0)), FAKE, FAKE, None, None, None) == 2
     assert L.m27q_matvec_q8(C.byref(W(m27q, rc=0)), FAKE, FAKE, None, None, None) == 2
+    assert L.m27q_matvec_q8(C.byref(W(m27q, rc=(1 << 24) + 1)), FAKE, FAKE, None, None, None) == 2
+    assert L.m27q_matvec_q8(C.byref(W(m27q, rb=(1 << 20) // 256 + 1)), FAKE, FAKE, None, None, None) == 2
     assert L.m27q_matvec_q8(C.byref(W(m27q, layout=7)), FAKE, FAKE, None, None, None) == 4
     assert L.m27q_matvec_q8(C.byref(W(m27q, ptr=FAKE + 2)), FAKE, FAKE, None, None, None) == 4
     assert L.m27q_matvec_q8(C.byref(ok), FAKE + 4, FAKE, None, None, None) == 4
