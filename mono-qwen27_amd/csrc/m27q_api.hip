@@ -229,6 +229,7 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     p.xd = a.d;
     p.xs = a.s;
     p.nmat = n;
+    if (few && n == 1) p.bal_wgs = matmul_mt_balance(tiles_of(ws[0].row_count), p.upr, cu_count());
     for (int i = 0; i < n; ++i) {
         p.W[i] = (const uint8_t *)ws[i].ptr;
         p.Y[i] = Ys[i];

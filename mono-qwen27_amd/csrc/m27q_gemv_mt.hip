@@ -33,15 +33,23 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     for (int k = 1; k < kMaxMulti; ++k)
         if (k < p.nmat && (int)blockIdx.x >= p.wg_start[k]) mi = k;
     const int rc = p.rc[mi];
-    const int tile0 = ((int)blockIdx.x - p.wg_start[mi]) * TPW;
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
+    // Tiles of this workgroup: TPW from tile0, or, with balanced tiling, nt
+    // of them (TPW - 1 or TPW); the slots past nt reread the workgroup's last
+    // tile (cache hits) and their rows are not written.
+    const int wg = (int)blockIdx.x - p.wg_start[mi];
+    int tile0 = wg * TPW, nt = TPW;
+    if (p.bal_wgs > 0) {
+        tile0 = (int)((long long)wg * ntiles / p.bal_wgs);
+        nt = (int)((long long)(wg + 1) * ntiles / p.bal_wgs) - tile0;
+    }
     const int U = p.upr / KS, rem = p.upr % KS;
     const int ub = ks * U + min(ks, rem);
     const int nu = U + (ks < rem ? 1 : 0);
 
     // First unit of weights before the staging, so their latencies overlap.
     const uint8_t *W[1] = {p.W[mi]};
-    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT> ws(W, tile0 + tg * WT, ntiles, rc, 0, p.upr, lane);
+    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, 0, p.upr, lane);
     typename T::Frag fa[1][WT], fb[1][WT];
     ws.load(fa, min(ub, p.upr - 1));
 
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
         float v = red[mt * KS * NR + rr];
 #pragma unroll
         for (int w = 1; w < KS; ++w) v += red[(mt * KS + w) * NR + rr];
-        if (row < rc && tok < p.M) {
+        if (row < rc && rr < nt * kTileRows && tok < p.M) {
             const size_t o = (size_t)tok * rc + row;
             p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
         }
@@ -158,7 +166,7 @@ static hipError_t launch_mt_cfg(MatmulMultiParams p, hipStream_t s) {
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
         p.wg_start[i] = total;
-        total += ((p.rc[i] + kTileRows - 1) / kTileRows + C::TPW - 1) / C::TPW;
+        total += p.bal_wgs > 0 ? p.bal_wgs : ((p.rc[i] + kTileRows - 1) / kTileRows + C::TPW - 1) / C::TPW;
     }
     p.wg_start[p.nmat] = total;
     const size_t lds = mt_lds<T, C, MT>(p.upr);
@@ -178,8 +186,21 @@ static int pick_mt_cfg(long long rows, int upr) {
     return rows <= 12288 ? kCfg84 : kCfg42;
 }
 
+// One matrix of short rows (< 40 units) with between 2 and 3 tiles per CU
+// spreads them over one workgroup per CU, as the M = 1 products do: o (640
+// tiles of 24 units) 8.55-8.67 us against 8.95-9.2 with (8, 1, 1).  Down (68
+// units) measured 1.8 us slower that way: one 12-wave workgroup per CU hides
+// less latency than 2.5 of (8, 1, 1).
+#ifndef M27Q_MT_BALANCE
+#define M27Q_MT_BALANCE 1
+#endif
+int matmul_mt_balance(long long tiles, int upr, int cus) {
+    return M27Q_MT_BALANCE && upr < 40 && tiles > 2LL * cus && tiles <= (long long)CfgB::TPW * cus ? cus : 0;
+}
+
 template <class T, int MT>
 static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
+    if (p.bal_wgs > 0) return launch_mt_cfg<T, CfgB, MT>(p, s);
 #ifdef M27Q_MT_CFG
     constexpr int forced = M27Q_MT_CFG;
     const int cfg = forced;
@@ -201,7 +222,7 @@ size_t matmul_mt_lds_bytes(uint32_t type, int upr) {
     auto one = [&](auto tag) -> size_t {
         using T = decltype(tag);
         return std::max({mt_lds<T, Cfg41, 2>(upr), mt_lds<T, Cfg81, 2>(upr), mt_lds<T, Cfg42, 2>(upr),
-                         mt_lds<T, Cfg84, 2>(upr)});
+                         mt_lds<T, Cfg84, 2>(upr), mt_lds<T, CfgB, 2>(upr)});
     };
     switch (type) {
         case kQ4_K: return one(Q4K{});

@@ -92,11 +92,17 @@ struct MatmulMultiParams {
     const int8_t *xq;
     const float *xd;
     const uint32_t *xs;
+    // few-token kernel only: when > 0, balanced tiling over this many
+    // workgroups for the one matrix (as GemvParams::bal)
+    int bal_wgs;
 };
 hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s);
 // Few-token products on the GEMV streaming structure (m27q_gemv_mt.hip): two
-// activation rows, TILED weights.
+// activation rows, TILED weights.  matmul_mt_balance(): the balanced
+// workgroup count for one matrix of `tiles` tiles of `upr` units on `cus`
+// CUs, or 0.
 size_t matmul_mt_lds_bytes(uint32_t type, int upr);
+int matmul_mt_balance(long long tiles, int upr, int cus);
 hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
 // int8-MFMA small-M products (m27q_mma.hip): TILED weights, any M (16 tokens
 // per launch).

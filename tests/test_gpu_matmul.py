@@ -32,6 +32,10 @@ CASES = [  # type, rows, K, M, layout
     # gate-sized rows at M = 3 (two sets per tile), the down shape at M = 12
     # (padding tokens in a 16-token launch), 17 tokens (16, then 1 on two sets)
     ("Q4_K", 17408, 5120, 3, 1), ("Q6_K", 5120, 17408, 12, 1), ("Q4_K", 8192, 512, 17, 1),
+    # few tokens with balanced tiling on 256 CUs (rows under 40 units): o (640
+    # tiles), and both ends of the range with a ragged last tile (513 and 768
+    # tiles)
+    ("Q4_K", 5120, 6144, 2, 1), ("Q6_K", 4100, 2048, 2, 1), ("Q4_K", 6141, 2048, 2, 1),
 ]
 
 
