@@ -290,7 +290,8 @@ def test_fp32_input_vs_oracle(m27q, ora, dev, type_name, rc, k):
 
 
 @pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 4100, 10240), ("Q4_K", 6141, 10240)])
-def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k):
+@pytest.mark.parametrize("layout", [0, 1])
+def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k, layout):
     """Balanced tiling at the ends of its range on 256 CUs: 513 tiles (one
     workgroup with 3, the rest with 2, which reread their last tile) and 768
     (3 each), both with a ragged last tile.  The quantized-input product
@@ -300,7 +301,7 @@ def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k):
     t = getattr(m27q, type_name)
     rb = k // m27q.BLOCK_ELEMS[t]
     wb = weights(ora, type_name, rc, k, 12)
-    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, layout, dev)
     x = np.random.default_rng(13).standard_normal(k).astype(np.float32)
     xd = to_dev(x, dev)
     act = m27q.Act(1, k, dev)
@@ -308,7 +309,7 @@ def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k):
     guard = np.float32(-7.25)
     y0 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
     y1 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
-    say("balanced tiling", type_name, rc, k)
+    say("balanced tiling", type_name, rc, k, layout)
     m27q.matvec_q8(w, act, y1[:rc])
     q, d, s = ora.quant_act(x)
     want, nrm = ora.gemv_act(t, wb, rb, rc, q, d, s)
