@@ -17,6 +17,7 @@ value = weight bytes of the layer (GGUF, unpadded: 214,671,360 B) / step time.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -110,6 +111,20 @@ def measured_traffic(kernel_label):
     for line in open(path):
         if line.startswith(kernel_label + ":"):
             return int(line.split()[-3])
+    return None
+
+
+def profiled_kernel_us(kernel_label):
+    """Average kernel duration (us) of one product in the committed rocprofv3
+    --kernel-trace summary; None where that summary is absent.  HIP events over
+    graph replays see the same kernel plus the gap to the next dispatch."""
+    path = os.path.join(ROOT, "profiles", "gemv_decode_layer_kernel_trace.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\s+" + re.escape(kernel_label) + r":.* avg\s+([0-9.]+) us", line)
+        if m:
+            return float(m.group(1))
     return None
 
 
@@ -412,6 +427,8 @@ def main():
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up"),
                      "traffic_source": "profiles/gemv_decode_layer_hbm_traffic.txt",
+                     "rocprof_kernel_avg_us": profiled_kernel_us("gate_up"),
+                     "rocprof_source": "profiles/gemv_decode_layer_kernel_trace.txt",
                      "avg_launch_us": dom["us"], "algorithmic_bytes": dom["bytes"]},
     }
     if not args.no_suite:
