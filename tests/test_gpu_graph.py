@@ -40,6 +40,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     f = torch.empty(2048, dtype=torch.float32, device=dev)
     fq = m27q.Act(1, 2048, dev)
     out = torch.empty(5120, dtype=torch.float32, device=dev)
+    out2 = torch.empty(5120, dtype=torch.float32, device=dev)
     act2 = m27q.Act(2, 5120, dev)
     Y2 = torch.empty((2, 1024), dtype=torch.float32, device=dev)
     act16 = m27q.Act(16, 5120, dev)
@@ -55,7 +56,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     idx = torch.empty(k, dtype=torch.int32, device=dev)
     val = torch.empty(k, dtype=torch.float32, device=dev)
     tok = torch.empty(1, dtype=torch.int32, device=dev)
-    outs = [x, qv, h, f, fq.buf, out, Y2, Y16, Y5, Y5q, Y5g, logits, idx, val, tok]
+    outs = [x, qv, h, f, fq.buf, out, out2, Y2, Y16, Y5, Y5q, Y5g, logits, idx, val, tok]
 
     def step(s):
         m27q.embed_rows(W["emb"], ids, x, bad, stream=s)
@@ -63,6 +64,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
         m27q.matvec(W["o"], qv, h, residual=x[1], stream=s)
         m27q.ffn_swiglu(W["gate"], W["up"], h, f, yq=fq, stream=s)
         m27q.matvec_q8(W["down"], fq, out, residual=h, stream=s)
+        m27q.matvec(W["down"], f, out2, residual=h, stream=s)  # the fp32 hand-off to down
         m27q.quant_act(x, act2, stream=s)
         m27q.matmul_q8(W["q"], act2, Y2, stream=s)
         m27q.quant_act(X16, act16, stream=s)
