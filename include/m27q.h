@@ -113,6 +113,42 @@ M27Q_API m27q_status m27q_unpack(uint32_t ggml_type, uint32_t row_blocks, uint32
  * would have (the writer is src/mono27b_blob.cpp:378-438). */
 M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path);
 
+/* One tensor of a .m27b weights section as a loader needs it: the entry's
+ * fields (include/mono27b_format.h:74-84), the layout from its reserved field,
+ * row_blocks as WeightView counts it (K / block size; K for F16 / F32; 0 when
+ * the entry's byte count is not whole rows of its type in its layout), and the
+ * absolute file offset of its bytes. */
+typedef struct m27q_blob_tensor {
+    char name[64];
+    uint32_t ggml_type;
+    uint32_t source_model;
+    uint32_t role;
+    uint32_t row_elems;
+    uint32_t row_count;
+    uint32_t layout;       /* M27Q_LAYOUT_GGUF or M27Q_LAYOUT_TILED (entry.reserved) */
+    uint32_t row_blocks;
+    uint32_t pad;
+    uint64_t file_offset;
+    uint64_t bytes;        /* entry.data_bytes */
+} m27q_blob_tensor;
+
+/* Reads and bounds-checks the blob's header, section table and weight entry
+ * table (host only).  *count gets the number of entries; the first
+ * min(cap, *count) are written to out (cap may be 0 to count only).  The
+ * table half of the reference's blob reader (mono27b_read_weights_section,
+ * src/mono27b_blob.cpp) for a loader of re-tiled blobs. */
+M27Q_API m27q_status m27q_blob_tensors(const char *path, m27q_blob_tensor *out, int cap, int *count);
+
+/* Uploads one tensor's bytes from the file to caller-owned device memory
+ * (dst_bytes >= t->bytes; 16-byte aligned for TILED) with synchronous
+ * host-to-device copies, and fills *w with the descriptor the products take
+ * (ptr = device_dst, layout = t->layout).  Not for graph capture: it reads a
+ * file.  Replaces lw() (exec:1695-1716), which copies a tensor's GGUF bytes
+ * into its own cudaMalloc; here the caller allocates (m27q_weight_bytes
+ * gives the size). */
+M27Q_API m27q_status m27q_blob_load(const char *path, const m27q_blob_tensor *t, void *device_dst,
+                                   size_t dst_bytes, m27q_weight *w);
+
 /* ------------------------------------------------------------------------
  * Activations
  * ---------------------------------------------------------------------- */
@@ -121,10 +157,11 @@ M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path)
  *   int8  codes[M][K]             at offset 0
  *   float d[M][K/32]              at offset m27q_act_d_offset(M, K)
  *   u32   sums[M][K/32]           at offset m27q_act_s_offset(M, K)
- * Per 32 values: d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0 (IEEE
- * divide), code = roundf(x * id) clamped to +-127 (the rule of ggml's
- * quantize_row_q8_1_ref), sums = (int16 sum of codes 0..15) | (int16 sum of
- * codes 16..31) << 16.  The reference's Q8_1 (exec:65-71) keeps an fp16 d and
+ * Per 32 values: d = amax/127 (IEEE divide), id = 1/d (IEEE divide) where
+ * that is finite, else 0 (d == 0, or a subnormal d below 2^-128: such a
+ * group's codes are all 0), code = roundf(x * id) clamped to +-127 (the rule
+ * of ggml's quantize_row_q8_1_ref), sums = (int16 sum of codes 0..15) |
+ * (int16 sum of codes 16..31) << 16.  The reference's Q8_1 (exec:65-71) keeps an fp16 d and
  * the float sum of x; this format keeps an fp32 d and the exact integer sums
  * its dot products use. */
 M27Q_API size_t m27q_act_bytes(int M, int K);
@@ -135,8 +172,11 @@ M27Q_API size_t m27q_act_s_offset(int M, int K);
  * :84-107). */
 M27Q_API m27q_status m27q_quant_act(const float *x, int M, int K, void *xq, hipStream_t stream);
 
-/* (x * sigmoid(gate)) -> xq.  Replaces k_quant_q8_1_fused_gate (exec:109-138,
- * site :2460). */
+/* (x * sigmoid(gate)) -> xq, the gate as x * (1 / (1 + e^-gate)) with a fixed
+ * exp (Cody-Waite range reduction and a degree-7 polynomial, argument clamped
+ * to [-87, 87]; within 2 ulp of e^t) in place of the reference's fast-math
+ * __expf, so the codes are reproducible bit for bit.  Replaces
+ * k_quant_q8_1_fused_gate (exec:109-138, site :2460). */
 M27Q_API m27q_status m27q_quant_act_gated(const float *x, const float *gate, int M, int K, void *xq,
                                           hipStream_t stream);
 
@@ -172,9 +212,15 @@ M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y,
 M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float *y, const float *residual,
                                     void *yq, hipStream_t stream);
 
-/* Up to 4 weights that share one activation (same type, layout, row_blocks),
- * in one launch: y[i] = W[i] x.  Replaces l_mv_pair (exec:2106-2125) and the
- * Wq || Wk, Wv pattern of the attention block (exec:2377-2395). */
+/* Up to 4 weights that share one activation (the same K; types and layouts
+ * may differ): y[i] = W[i] x.  Weights of one type and layout run in one
+ * launch; each further (type, layout) group is one more launch on the same
+ * stream, in order of first appearance, on the same activation codes.  Every
+ * weight is checked before the first launch.  Replaces l_mv_pair
+ * (exec:2106-2125), whose pair mixes types on the SSM layers (wqkv Q6_K and
+ * wqkv_gate Q5_K in the UD-Q4_K_XL file, exec:2492; a member l_mv_pair skips,
+ * null or with no rows, is left out: n = 1), and the Wq || Wk, Wv pattern of
+ * the attention block (exec:2377-2395). */
 M27Q_API m27q_status m27q_matvec_multi(int n, const m27q_weight *ws, const float *x, float *const *ys,
                                        hipStream_t stream);
 M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
@@ -215,9 +261,10 @@ M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float
 M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y,
                                     const float *residual, hipStream_t stream);
 
-/* Up to 4 TILED weights of one type and K on the same M activation rows, in
- * one launch: Ys[i] = X W[i]^T ([M][row_count_i] each).  The small-M
- * counterpart of m27q_matvec_q8_multi (q/k/v, gate/up of a verify batch). */
+/* Up to 4 TILED weights of one K on the same M activation rows: Ys[i] = X
+ * W[i]^T ([M][row_count_i] each), one launch per weight type as in
+ * m27q_matvec_q8_multi.  The small-M counterpart of m27q_matvec_q8_multi
+ * (q/k/v, gate/up of a verify batch). */
 M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
                                           hipStream_t stream);
 
@@ -256,7 +303,8 @@ M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, 
 /* On-device token choice from m27q_topk's candidates (idx/val in rank order,
  * 1 <= k <= 64), the steps of sample() (src/mono27b_chat.cpp:203-270) after its
  * top-k: temperature <= 0 gives idx[0] (the argmax, first index on ties);
- * otherwise p_i = expf((val_i - val_0) / temperature), normalized; candidates
+ * otherwise p_i = e^((val_i - val_0) / temperature) (the fixed exp of
+ * m27q_quant_act_gated; 0 below e^-87), normalized; candidates
  * with p_i < p_0 * min_p are dropped; top_p < 1 keeps the shortest prefix whose
  * running sum reaches top_p; the token is the first candidate whose running sum
  * reaches u * (sum of the kept p).  u is a device float in [0, 1), token a

@@ -1,8 +1,8 @@
 // m27q_act.hip -- fp32 activations -> per-32 int8 codes with fp32 scale.
 //
 // One lane per value, one 32-lane half-wave per group: amax by cross-lane max,
-// d = amax/127 (IEEE divide), code = roundf(x/d) clamped to +-127, and the two
-// 16-code integer sums.  Replaces k_quant_q8_1 / k_quant_q8_1_fused_gate
+// d = amax/127 (IEEE divide), code = roundf(x * (1/d)) clamped to +-127 (the
+// rule of quant32 in m27q_device.h), and the two 16-code integer sums.  Replaces k_quant_q8_1 / k_quant_q8_1_fused_gate
 // (exec:84-107, :109-138), which keep an fp16 scale and the float sum of x.
 #include "m27q_internal.h"
 #include "m27q_device.h"

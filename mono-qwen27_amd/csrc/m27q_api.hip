@@ -106,9 +106,10 @@ m27q_status check_out_quant(const m27q_weight *w, const void *yq) {
 
 // Shared body of every integer-dot M = 1 product.  n weights of one type,
 // layout and K share the activation (fp32 x, or the quantized xq); with
-// swiglu, ws = {gate, up} and ys[0] receives silu(gate x) * (up x).
+// swiglu, ws = {gate, up} and ys[0] receives silu(gate x) * (up x).  With
+// dry, every check runs and nothing is launched.
 m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float *x, float *const *ys,
-                      const float *residual, bool swiglu, void *yq, hipStream_t stream) {
+                      const float *residual, bool swiglu, void *yq, hipStream_t stream, bool dry = false) {
     if (!ws || !ys) return M27Q_ERR_NULL;
     if (n < 1 || n > kMaxMulti || (swiglu && n != 2)) return M27Q_ERR_SHAPE;
     for (int i = 0; i < n; ++i) {
@@ -157,6 +158,7 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
                         : pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,
                                         rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
+    if (dry) return M27Q_OK;
     if (x) {
         p.x = x;
     } else {
@@ -203,7 +205,7 @@ constexpr int kMtMaxM = M27Q_MT_MAXM;
 constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU
 
 m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
-                              const float *const *res, hipStream_t stream) {
+                              const float *const *res, hipStream_t stream, bool dry = false) {
     for (int i = 0; i < n; ++i) {
         const m27q_status st = check_weight(&ws[i], true);
         if (st != M27Q_OK) return st;
@@ -224,6 +226,7 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     // below it.
     for (int i = 0; i < n && !few; ++i)
         if (tiled_bytes(ws[i].ggml_type, ws[i].row_blocks, ws[i].row_count) >= (1ull << 32)) return M27Q_ERR_SHAPE;
+    if (dry) return M27Q_OK;
     const ActView a = act_view(xq, M, p.K);
     p.xq = a.q;
     p.xd = a.d;
@@ -238,6 +241,47 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     }
     return hip_status(few ? launch_matmul_mt(ws[0].ggml_type, p, stream)
                           : launch_matmul_mfma(ws[0].ggml_type, p, stream));
+}
+
+// Up to kMaxMulti weights of one K sharing one activation, of any mix of
+// types and layouts (l_mv_pair runs wqkv and wqkv_gate of different types on
+// one quantized x, exec:2106-2125, :2492): each (type, layout) group is one
+// launch, in order of first appearance, on the same stream.  Every group is
+// checked before the first launch.  M == 0 selects the M = 1 products.
+m27q_status grouped_multi(int n, const m27q_weight *ws, int M, const void *xq, const float *x, float *const *ys,
+                          hipStream_t stream) {
+    if (!ws || !ys) return M27Q_ERR_NULL;
+    if (n < 1 || n > kMaxMulti) return M27Q_ERR_SHAPE;
+    for (int i = 0; i < n; ++i) {
+        const m27q_status st = check_weight(&ws[i], true);
+        if (st != M27Q_OK) return st;
+        if (k_of(&ws[i]) != k_of(&ws[0])) return M27Q_ERR_SHAPE;
+    }
+    int group[kMaxMulti], ng = 0;
+    for (int i = 0; i < n; ++i) {
+        group[i] = -1;
+        for (int j = 0; j < i && group[i] < 0; ++j)
+            if (ws[j].ggml_type == ws[i].ggml_type && ws[j].layout == ws[i].layout) group[i] = group[j];
+        if (group[i] < 0) group[i] = ng++;
+    }
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int g = 0; g < ng; ++g) {
+            m27q_weight gw[kMaxMulti];
+            float *gy[kMaxMulti];
+            const float *gr[kMaxMulti] = {nullptr, nullptr, nullptr, nullptr};
+            int m = 0;
+            for (int i = 0; i < n; ++i)
+                if (group[i] == g) {
+                    gw[m] = ws[i];
+                    gy[m++] = ys[i];
+                }
+            const bool dry = pass == 0;
+            const m27q_status st = M == 0 ? gemv_impl(m, gw, xq, x, gy, nullptr, false, nullptr, stream, dry)
+                                          : matmul_multi_impl(m, gw, M, xq, gy, gr, stream, dry);
+            if (st != M27Q_OK) return st;
+        }
+    }
+    return M27Q_OK;
 }
 
 }  // namespace
@@ -282,7 +326,7 @@ M27Q_API m27q_status m27q_matvec_q8(const m27q_weight *w, const void *xq, float 
 M27Q_API m27q_status m27q_matvec_q8_multi(int n, const m27q_weight *ws, const void *xq, float *const *ys,
                                           hipStream_t stream) {
     if (!xq) return M27Q_ERR_NULL;
-    return gemv_impl(n, ws, xq, nullptr, ys, nullptr, false, nullptr, stream);
+    return grouped_multi(n, ws, 0, xq, nullptr, ys, stream);
 }
 
 M27Q_API m27q_status m27q_ffn_swiglu_q8(const m27q_weight *gate, const m27q_weight *up, const void *xq, float *y,
@@ -329,7 +373,7 @@ M27Q_API m27q_status m27q_matvec(const m27q_weight *w, const float *x, float *y,
 M27Q_API m27q_status m27q_matvec_multi(int n, const m27q_weight *ws, const float *x, float *const *ys,
                                        hipStream_t stream) {
     if (!x) return M27Q_ERR_NULL;
-    return gemv_impl(n, ws, nullptr, x, ys, nullptr, false, nullptr, stream);
+    return grouped_multi(n, ws, 0, nullptr, x, ys, stream);
 }
 
 M27Q_API m27q_status m27q_ffn_swiglu(const m27q_weight *gate, const m27q_weight *up, const float *x, float *y,
@@ -375,8 +419,7 @@ M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, c
     for (int i = 0; i < n; ++i)
         if (ws[i].layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
     if (M == 1) return m27q_matvec_q8_multi(n, ws, xq, Ys, stream);
-    const float *rs[kMaxMulti] = {nullptr, nullptr, nullptr, nullptr};
-    return matmul_multi_impl(n, ws, M, xq, Ys, rs, stream);
+    return grouped_multi(n, ws, M, xq, nullptr, Ys, stream);
 }
 
 static m27q_status gather_impl(const m27q_weight *w, const int32_t *ids, int row0, int n, float *out,

@@ -10,11 +10,15 @@
 // reserved field (0 GGUF, 1 TILED) and each tensor 256-byte aligned; every
 // other byte (header fields, tokenizer, non-matrix tensors) is copied.  The
 // result still passes the reference's own blob validation and entry reads.
-// The record layouts below must stay byte-identical to the reference's
-// structs: they are the file format.
+// m27q_blob_tensors / m27q_blob_load are the loader's side: the entry table
+// as weight descriptors (the layout from the reserved field) and one
+// tensor's bytes uploaded to caller-owned device memory, the role of lw()
+// for a blob.  The record layouts below must stay byte-identical to the
+// reference's structs: they are the file format.
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <vector>
 
 #include "../../include/m27q.h"
@@ -86,49 +90,66 @@ bool zeros(const File &out, uint64_t n) {
     return true;
 }
 
+constexpr uint32_t kMaxRows = 1u << 24;   // the products' row limit
+constexpr uint32_t kMaxRowElems = 1u << 20;
+
 // A matrix entry whose bytes are whole GGUF rows of a type with a TILED form.
 bool retilable(const WeightEntry &e) {
-    if (e.reserved != M27Q_LAYOUT_GGUF || !is_quant(e.ggml_type) || e.row_elems == 0 || e.row_count == 0) return false;
+    if (e.reserved != M27Q_LAYOUT_GGUF || !is_quant(e.ggml_type) || e.row_elems == 0 || e.row_count == 0 ||
+        e.row_count > kMaxRows || e.row_elems > kMaxRowElems)
+        return false;
     const int be = block_elems(e.ggml_type);
     if (e.row_elems % (uint32_t)be) return false;
     return e.data_bytes == (uint64_t)e.row_count * (e.row_elems / be) * block_bytes(e.ggml_type);
 }
 
-}  // namespace
+// The blob's table: header, section table, the weights section's header and
+// entries.  Every offset read from the file is checked without overflow.
+struct Table {
+    BlobHeader h;
+    std::vector<BlobSection> secs;
+    int wi = -1;  // index of the weights section
+    WeightsSection wh;
+    std::vector<WeightEntry> ents;
+};
 
-extern "C" {
+m27q_status read_table(const File &in, Table &t) {
+    if (!in.read(&t.h, sizeof(t.h)) || t.h.magic != kBlobMagic || t.h.section_count == 0 || t.h.section_count > 64)
+        return M27Q_ERR_IO;
+    t.secs.resize(t.h.section_count);
+    if (!in.seek(t.h.section_table_offset) || !in.read(t.secs.data(), t.secs.size() * sizeof(BlobSection)))
+        return M27Q_ERR_IO;
+    for (int i = 0; i < (int)t.secs.size(); ++i)
+        if (t.secs[i].kind == kSectionWeights) t.wi = i;
+    if (t.wi < 0) return M27Q_ERR_IO;
+    const BlobSection &ws = t.secs[t.wi];
+    // The weights section is the file's tail (as mono27b_write_stub_blob lays
+    // it out), and the section table sits before it.
+    const uint64_t table_bytes = t.secs.size() * sizeof(BlobSection);
+    if (ws.offset > t.h.file_bytes || ws.bytes != t.h.file_bytes - ws.offset || t.h.section_table_offset > ws.offset ||
+        table_bytes > ws.offset - t.h.section_table_offset || ws.bytes < sizeof(WeightsSection))
+        return M27Q_ERR_IO;
+    if (!in.seek(ws.offset) || !in.read(&t.wh, sizeof(t.wh)) || t.wh.magic != kWeightsMagic ||
+        t.wh.entry_count == 0 || t.wh.entry_count > (1u << 20) ||
+        (uint64_t)t.wh.entry_count * sizeof(WeightEntry) > ws.bytes - sizeof(WeightsSection))
+        return M27Q_ERR_IO;
+    t.ents.resize(t.wh.entry_count);
+    if (!in.read(t.ents.data(), t.ents.size() * sizeof(WeightEntry))) return M27Q_ERR_IO;
+    for (const WeightEntry &e : t.ents)
+        if (e.data_offset > ws.bytes || e.data_bytes > ws.bytes - e.data_offset) return M27Q_ERR_IO;
+    return M27Q_OK;
+}
 
-M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path) {
-    if (!in_path || !out_path) return M27Q_ERR_NULL;
-    if (!std::strcmp(in_path, out_path)) return M27Q_ERR_IO;
+m27q_status retile(const char *in_path, const char *out_path) {
     const File in(in_path, "rb");
     if (!in.f) return M27Q_ERR_IO;
-    BlobHeader h;
-    if (!in.read(&h, sizeof(h)) || h.magic != kBlobMagic || h.section_count == 0 || h.section_count > 64)
-        return M27Q_ERR_IO;
-    std::vector<BlobSection> secs(h.section_count);
-    if (!in.seek(h.section_table_offset) || !in.read(secs.data(), secs.size() * sizeof(BlobSection)))
-        return M27Q_ERR_IO;
-    int wi = -1;
-    for (int i = 0; i < (int)secs.size(); ++i)
-        if (secs[i].kind == kSectionWeights) wi = i;
-    if (wi < 0) return M27Q_ERR_IO;
-    const BlobSection ws = secs[wi];
-    // The weights section must be the file's tail (as mono27b_write_stub_blob
-    // lays it out), and the section table must sit before it.
-    if (ws.offset + ws.bytes != h.file_bytes || h.section_table_offset + secs.size() * sizeof(BlobSection) > ws.offset)
-        return M27Q_ERR_IO;
-    WeightsSection wh;
-    if (!in.seek(ws.offset) || !in.read(&wh, sizeof(wh)) || wh.magic != kWeightsMagic || wh.entry_count == 0 ||
-        wh.entry_count > (1u << 20))
-        return M27Q_ERR_IO;
-    std::vector<WeightEntry> ents(wh.entry_count), outs;
-    if (!in.read(ents.data(), ents.size() * sizeof(WeightEntry))) return M27Q_ERR_IO;
-    for (const WeightEntry &e : ents)
-        if (e.data_offset + e.data_bytes > ws.bytes) return M27Q_ERR_IO;
+    Table t;
+    if (const m27q_status st = read_table(in, t); st != M27Q_OK) return st;
+    const BlobSection ws = t.secs[t.wi];
+    const std::vector<WeightEntry> &ents = t.ents;
 
     // New entry table: offsets relative to the weights section, 256-aligned.
-    outs = ents;
+    std::vector<WeightEntry> outs = ents;
     uint64_t pos = sizeof(WeightsSection) + ents.size() * sizeof(WeightEntry);
     for (WeightEntry &e : outs) {
         pos = (pos + kAlign - 1) / kAlign * kAlign;
@@ -141,17 +162,18 @@ M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path)
     }
     BlobSection ws2 = ws;
     ws2.bytes = pos;
-    BlobHeader h2 = h;
+    BlobHeader h2 = t.h;
     h2.file_bytes = ws.offset + pos;
-    std::vector<BlobSection> secs2 = secs;
-    secs2[wi] = ws2;
+    std::vector<BlobSection> secs2 = t.secs;
+    secs2[t.wi] = ws2;
 
     const File out(out_path, "wb");
     if (!out.f) return M27Q_ERR_IO;
     // Everything before the weights section, with the updated header and table.
     if (!copy_range(in, 0, ws.offset, out) || !out.seek(0) || !out.write(&h2, sizeof(h2)) ||
-        !out.seek(h.section_table_offset) || !out.write(secs2.data(), secs2.size() * sizeof(BlobSection)) ||
-        !out.seek(ws.offset) || !out.write(&wh, sizeof(wh)) || !out.write(outs.data(), outs.size() * sizeof(WeightEntry)))
+        !out.seek(t.h.section_table_offset) || !out.write(secs2.data(), secs2.size() * sizeof(BlobSection)) ||
+        !out.seek(ws.offset) || !out.write(&t.wh, sizeof(t.wh)) ||
+        !out.write(outs.data(), outs.size() * sizeof(WeightEntry)))
         return M27Q_ERR_IO;
     uint64_t at = sizeof(WeightsSection) + outs.size() * sizeof(WeightEntry);
     std::vector<uint8_t> src, dst;
@@ -172,6 +194,103 @@ M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path)
         at = o.data_offset + o.data_bytes;
     }
     return std::fflush(out.f) == 0 ? M27Q_OK : M27Q_ERR_IO;
+}
+
+// Row blocks of an entry as the products count them (K for F32 / F16), as
+// lw() sets WeightView::row_blocks (exec:1706-1707); 0 if the entry's bytes
+// are not whole rows of its type in its layout.
+uint32_t entry_row_blocks(const WeightEntry &e) {
+    if (e.row_elems == 0 || e.row_count == 0 || e.row_count > kMaxRows || e.row_elems > kMaxRowElems) return 0;
+    const int be = block_elems(e.ggml_type);
+    if (be == 0 || e.row_elems % (uint32_t)be) return 0;
+    const uint32_t rb = e.row_elems / (uint32_t)be;
+    uint64_t want = 0;
+    if (e.reserved == M27Q_LAYOUT_TILED) {
+        if (!is_quant(e.ggml_type)) return 0;
+        want = tiled_bytes(e.ggml_type, rb, e.row_count);
+    } else if (e.reserved == M27Q_LAYOUT_GGUF) {
+        want = (uint64_t)e.row_count * rb * (uint64_t)block_bytes(e.ggml_type);
+    }
+    return want != 0 && e.data_bytes == want ? rb : 0;
+}
+
+m27q_status tensors(const char *path, m27q_blob_tensor *out, int cap, int *count) {
+    const File in(path, "rb");
+    if (!in.f) return M27Q_ERR_IO;
+    Table t;
+    if (const m27q_status st = read_table(in, t); st != M27Q_OK) return st;
+    *count = (int)t.ents.size();
+    for (int i = 0; i < (int)t.ents.size() && i < cap; ++i) {
+        const WeightEntry &e = t.ents[i];
+        m27q_blob_tensor &o = out[i];
+        std::memset(&o, 0, sizeof(o));
+        std::memcpy(o.name, e.name, sizeof(o.name));
+        o.name[sizeof(o.name) - 1] = '\0';
+        o.ggml_type = e.ggml_type;
+        o.source_model = e.source_model;
+        o.role = e.role;
+        o.row_elems = e.row_elems;
+        o.row_count = e.row_count;
+        o.layout = e.reserved;
+        o.row_blocks = entry_row_blocks(e);
+        o.file_offset = t.secs[t.wi].offset + e.data_offset;
+        o.bytes = e.data_bytes;
+    }
+    return M27Q_OK;
+}
+
+m27q_status load(const char *path, const m27q_blob_tensor *t, void *dst, size_t dst_bytes, m27q_weight *w) {
+    if (t->row_blocks == 0 || block_elems(t->ggml_type) == 0 || t->row_count == 0) return M27Q_ERR_TYPE;
+    if (t->layout != M27Q_LAYOUT_GGUF && t->layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
+    if (t->layout == M27Q_LAYOUT_TILED && (uintptr_t)dst % 16) return M27Q_ERR_LAYOUT;
+    if (t->bytes != m27q_weight_bytes(t->ggml_type, t->row_blocks, t->row_count, t->layout)) return M27Q_ERR_SHAPE;
+    if (dst_bytes < t->bytes) return M27Q_ERR_SHAPE;
+    const File in(path, "rb");
+    if (!in.f || !in.seek(t->file_offset)) return M27Q_ERR_IO;
+    // Staged through host memory in chunks, as lw() copies its mapped bytes
+    // with one synchronous cudaMemcpy (exec:1712).
+    std::vector<uint8_t> buf((size_t)std::min<uint64_t>(t->bytes, kCopyChunk));
+    for (uint64_t off = 0; off < t->bytes;) {
+        const size_t c = (size_t)std::min<uint64_t>(t->bytes - off, buf.size());
+        if (!in.read(buf.data(), c)) return M27Q_ERR_IO;
+        if (hipMemcpy((uint8_t *)dst + off, buf.data(), c, hipMemcpyHostToDevice) != hipSuccess) return M27Q_ERR_HIP;
+        off += c;
+    }
+    *w = m27q_weight{dst, t->ggml_type, t->row_blocks, t->row_count, t->layout};
+    return M27Q_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path) {
+    if (!in_path || !out_path) return M27Q_ERR_NULL;
+    if (!std::strcmp(in_path, out_path)) return M27Q_ERR_IO;
+    try {
+        return retile(in_path, out_path);
+    } catch (const std::bad_alloc &) {
+        return M27Q_ERR_IO;
+    }
+}
+
+M27Q_API m27q_status m27q_blob_tensors(const char *path, m27q_blob_tensor *out, int cap, int *count) {
+    if (!path || !count || (cap > 0 && !out)) return M27Q_ERR_NULL;
+    try {
+        return tensors(path, out, cap, count);
+    } catch (const std::bad_alloc &) {
+        return M27Q_ERR_IO;
+    }
+}
+
+M27Q_API m27q_status m27q_blob_load(const char *path, const m27q_blob_tensor *t, void *device_dst, size_t dst_bytes,
+                                    m27q_weight *w) {
+    if (!path || !t || !device_dst || !w) return M27Q_ERR_NULL;
+    try {
+        return load(path, t, device_dst, dst_bytes, w);
+    } catch (const std::bad_alloc &) {
+        return M27Q_ERR_IO;
+    }
 }
 
 }  // extern "C"

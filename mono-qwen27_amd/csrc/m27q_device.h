@@ -11,9 +11,40 @@ namespace m27q {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
+// e^t, with t clamped to [-87, 87] (NaN is taken as -87), so that 2^n and
+// the result stay normal floats.  Cody-Waite range reduction (W. J. Cody and
+// W. Waite, Software Manual for the Elementary Functions, 1980):
+// n = rint(t log2 e), r = t - n ln2 with ln2 split into a float and the
+// float of its remainder (the first FMA is exact), then the degree-7 Taylor
+// polynomial of e^r on |r| <= ln2 / 2 (truncation below 1e-8 relative) by
+// Horner's rule in FMAs, times 2^n built from its exponent bits.  Every step
+// is an IEEE operation with one rounding (multiply, FMA, rint), nothing is
+// contracted, so the host oracle's restatement of the same sequence gives the
+// same bits; within 2 ulp of e^t.
+__device__ __forceinline__ float exp_cw(float t) {
+#pragma clang fp contract(off)
+    t = fminf(fmaxf(t, -87.0f), 87.0f);
+    const float n = __builtin_rintf(t * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e430p-1f, t);
+    r = __builtin_fmaf(-n, -0x1.05c610p-29f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return p * __int_as_float(((int)n + 127) << 23);
+}
+
 // x * sigmoid(g), the gated activation of k_quant_q8_1_fused_gate
-// (exec:109-138); the one definition both quantizer kernels use.
-__device__ __forceinline__ float gated(float x, float g) { return x * (1.0f / (1.0f + expf(-g))); }
+// (exec:109-138, x * (1 / (1 + e^-g))); the one definition both quantizer
+// kernels use.  IEEE divide and multiply, e^-g from exp_cw.
+__device__ __forceinline__ float gated(float x, float g) {
+#pragma clang fp contract(off)
+    return x * (1.0f / (1.0f + exp_cw(-g)));
+}
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     const uint16_t b = (uint16_t)bits16;
@@ -67,20 +98,28 @@ __device__ __forceinline__ float sum8(float v) {
 // ---------------------------------------------------------------------------
 // Per-32 activation quantization.  The rule (fixed here and restated by the
 // oracle): d = amax / 127 (IEEE divide), id = 1 / d (IEEE divide; 0 when
-// d == 0), code = roundf(x * id) (one fp32 multiply, round half away from
-// zero), clamped to +-127.  This is the rule of ggml's reference quantizer
+// that is not finite: d == 0, or a subnormal d below 2^-128), code =
+// roundf(x * id) (one fp32 multiply, round half away from zero), clamped to
+// +-127.  A group whose id is 0 has all codes 0 (its values are below
+// 3.7e-37 in magnitude).  This is the rule of ggml's reference quantizer
 // quantize_row_q8_1_ref; the reference's GPU kernel (exec:84-107) writes
 // roundf(x / d) under fast-math, which compiles to the same multiply by an
 // approximate reciprocal.  Besides d, the two 16-value integer code sums are
 // kept, packed as (int16 lo) | (int16 hi) << 16.
+// 1 / d where that is finite, else 0 (d == 0 gives +inf first).
+__device__ __forceinline__ float inv_scale(float d) {
+    const float r = 1.0f / d;
+    return r < __builtin_inff() ? r : 0.0f;
+}
+
 // roundf(x * id) clamped to +-127.  For |v| < 2^23, (int)(v + copysign(h, v))
 // with h = 0.49999997f (the largest float below 0.5) equals (int)roundf(v):
 // checked over every such float.  Below 0.5 the sum stays below 1; from 0.5
 // on it lands in the right unit interval, ties going away from zero.  The
 // product and the sum are each rounded once, as the host oracle's x * id and
 // roundf are: contracting them into an FMA (the default for HIP) would skip
-// the product's rounding.  |v| stays below 128 here; the clamp handles the
-// saturated conversion of a subnormal scale's 1/d.
+// the product's rounding.  id is finite (inv_scale), so |v| <= 127 (1 + 2^-21)
+// even for a subnormal d, and the conversion is always defined.
 __device__ __forceinline__ int quant_code(float x, float id) {
 #pragma clang fp contract(off)
     const float v = x * id;
@@ -120,7 +159,7 @@ __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
 #pragma unroll
     for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
     const float d = div127(amax);
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = inv_scale(d);
     const int q = quant_code(v, id);
     int s = q;
 #pragma unroll
@@ -143,7 +182,7 @@ __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uin
     amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
     amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
     const float d = div127(amax);
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = inv_scale(d);
     const int q0 = quant_code(a.x, id), q1 = quant_code(a.y, id), q2 = quant_code(a.z, id), q3 = quant_code(a.w, id);
     const int q4 = quant_code(b.x, id), q5 = quant_code(b.y, id), q6 = quant_code(b.z, id), q7 = quant_code(b.w, id);
     int s = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));

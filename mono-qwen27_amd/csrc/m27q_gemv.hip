@@ -125,7 +125,11 @@ __device__ __forceinline__ int stage_span(int Kp) {
     return XF32 ? Kp / 8 : Kp / 16;  // slots needed for the whole activation
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// silu(g) = g / (1 + e^-g), e^-g from exp_cw (the gated quantizer's exp).
+__device__ __forceinline__ float silu(float g) {
+#pragma clang fp contract(off)
+    return g / (1.0f + exp_cw(-g));
+}
 
 template <class T, int NM, int TPW>
 __device__ __forceinline__ void compute_unit(const typename T::Frag (&f)[NM][TPW], const ActLds &act, int u,

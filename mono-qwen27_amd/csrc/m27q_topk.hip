@@ -308,9 +308,10 @@ __global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__re
 
 // Sampling from the top-k candidates, in the steps and order of sample()
 // (src/mono27b_chat.cpp:203-270) after its top-k: probabilities
-// expf((v_i - v_0) / T) computed per lane, then one lane runs the sum, the
-// normalization, the min_p and top_p cuts and the pick in candidate order, so
-// the float sums round as the reference's sequential loop does.
+// e^((v_i - v_0) / T) computed per lane (exp_cw; 0 below e^-87, NaN kept),
+// then one lane runs the sum, the normalization, the min_p and top_p cuts and
+// the pick in candidate order, so the float sums round as the reference's
+// sequential loop does.
 __global__ __launch_bounds__(kWave) void k_sample(const int32_t *__restrict__ idx, const float *__restrict__ val,
                                                   int k, float temperature, float min_p, float top_p,
                                                   const float *__restrict__ u, int32_t *__restrict__ token) {
@@ -322,7 +323,10 @@ __global__ __launch_bounds__(kWave) void k_sample(const int32_t *__restrict__ id
         if (lane == 0) *token = best;
         return;
     }
-    if (lane < k) p[lane] = expf((val[lane] - val[0]) / temperature);
+    if (lane < k) {
+        const float a = (val[lane] - val[0]) / temperature;
+        p[lane] = a >= -87.0f ? exp_cw(a) : (a < -87.0f ? 0.0f : a);
+    }
     __syncthreads();
     if (lane != 0) return;
     float sum = 0.f;

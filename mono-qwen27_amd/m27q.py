@@ -37,6 +37,14 @@ class WeightDesc(C.Structure):
                 ("row_count", C.c_uint32), ("layout", C.c_uint32)]
 
 
+class BlobTensor(C.Structure):
+    """m27q_blob_tensor: one entry of a .m27b weights section."""
+    _fields_ = [("name", C.c_char * 64), ("ggml_type", C.c_uint32), ("source_model", C.c_uint32),
+                ("role", C.c_uint32), ("row_elems", C.c_uint32), ("row_count", C.c_uint32),
+                ("layout", C.c_uint32), ("row_blocks", C.c_uint32), ("pad", C.c_uint32),
+                ("file_offset", C.c_uint64), ("bytes", C.c_uint64)]
+
+
 _P, _I, _SZ, _U32 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint32
 _SIGS = {
     "m27q_status_string": (C.c_char_p, [_I]),
@@ -45,6 +53,8 @@ _SIGS = {
     "m27q_repack": (_I, [_U32, _U32, _U32, _P, _P]),
     "m27q_unpack": (_I, [_U32, _U32, _U32, _P, _P]),
     "m27q_retile_blob": (_I, [C.c_char_p, C.c_char_p]),
+    "m27q_blob_tensors": (_I, [C.c_char_p, C.POINTER(BlobTensor), _I, C.POINTER(_I)]),
+    "m27q_blob_load": (_I, [C.c_char_p, C.POINTER(BlobTensor), _P, _SZ, C.POINTER(WeightDesc)]),
     "m27q_act_bytes": (_SZ, [_I, _I]),
     "m27q_act_d_offset": (_SZ, [_I, _I]),
     "m27q_act_s_offset": (_SZ, [_I, _I]),
@@ -124,6 +134,15 @@ def retile_blob(in_path: str, out_path: str) -> None:
     check(lib().m27q_retile_blob(in_path.encode(), out_path.encode()), "m27q_retile_blob")
 
 
+def blob_tensors(path: str) -> list:
+    """The entry table of a .m27b blob as BlobTensor records (host only)."""
+    n = C.c_int(0)
+    check(lib().m27q_blob_tensors(path.encode(), None, 0, C.byref(n)), "m27q_blob_tensors")
+    out = (BlobTensor * n.value)()
+    check(lib().m27q_blob_tensors(path.encode(), out, n.value, C.byref(n)), "m27q_blob_tensors")
+    return list(out)
+
+
 def act_bytes(M: int, K: int) -> int:
     return lib().m27q_act_bytes(M, K)
 
@@ -174,6 +193,16 @@ class Weight:
             host = repack(type_, rb, rc, host)
         data = torch.from_numpy(host).to(device)
         return Weight(data, type_, rb, rc, layout)
+
+
+def blob_load(path: str, t: BlobTensor, device="cuda") -> Weight:
+    """Upload one blob tensor (m27q_blob_load) into a new device buffer."""
+    torch = _torch()
+    data = torch.empty(max(1, int(t.bytes)), dtype=torch.uint8, device=device)
+    d = WeightDesc()
+    check(lib().m27q_blob_load(path.encode(), C.byref(t), data.data_ptr(), data.numel(), C.byref(d)),
+          "m27q_blob_load")
+    return Weight(data, d.ggml_type, d.row_blocks, d.row_count, d.layout)
 
 
 class Act:

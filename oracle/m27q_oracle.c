@@ -445,7 +445,8 @@ static void quant_group32(const float *x, int8_t *q, float *d, uint32_t *s) {
         if (a > amax) amax = a;
     }
     const float dd = amax / 127.f;
-    const float id = dd != 0.f ? 1.0f / dd : 0.f;
+    const float r = 1.0f / dd;                 /* +inf for dd == 0 */
+    const float id = r < INFINITY ? r : 0.f;   /* not finite: every code 0 */
     int lo = 0, hi = 0;
     for (int l = 0; l < 32; ++l) {
         const float t = x[l] * id;
@@ -461,13 +462,47 @@ void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s) 
     for (int64_t j = 0; j < k / 32; ++j) quant_group32(x + 32 * j, q + 32 * j, d + j, s + j);
 }
 
+/* e^t with t clamped to [-87, 87] (NaN taken as -87): the build's fixed exp,
+ * so that host and device agree bit for bit.  Cody-Waite range reduction
+ * (W. J. Cody and W. Waite, Software Manual for the Elementary Functions,
+ * 1980): n = rint(t log2 e), r = t - n ln2 with ln2 = hi + lo in two floats
+ * (the first FMA is exact), the degree-7 Taylor polynomial of e^r by Horner's
+ * rule in FMAs, then the exact scaling by 2^n (n in [-126, 126], so 2^n and
+ * the result are normal).  Pinned in tests/test_oracle.py against float64
+ * exp (within 2 ulp over the whole range and at the clamp ends). */
+float ora_exp_cw(float t) {
+    t = fminf(fmaxf(t, -87.0f), 87.0f);
+    const float n = rintf(t * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e430p-1f, t);
+    r = fmaf(-n, -0x1.05c610p-29f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    union { uint32_t u; float f; } sc = { (uint32_t)((int)n + 127) << 23 };
+    return p * sc.f;
+}
+
+/* x * (1 / (1 + e^-g)): k_quant_q8_1_fused_gate's gate (exec:119), with the
+ * build's fixed exp in place of the fast-math __expf. */
+float ora_gated(float x, float g) { return x * (1.0f / (1.0f + ora_exp_cw(-g))); }
+
+void ora_exp_cw_n(const float *t, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ora_exp_cw(t[i]);
+}
+
+void ora_gated_n(const float *x, const float *g, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ora_gated(x[i], g[i]);
+}
+
 void ora_quant_act_gated(const float *x, const float *g, int64_t k, int8_t *q, float *d, uint32_t *s) {
     float t[32];
     for (int64_t j = 0; j < k / 32; ++j) {
-        for (int l = 0; l < 32; ++l) {
-            const float sig = 1.0f / (1.0f + expf(-g[32 * j + l]));
-            t[l] = x[32 * j + l] * sig;
-        }
+        for (int l = 0; l < 32; ++l) t[l] = ora_gated(x[32 * j + l], g[32 * j + l]);
         quant_group32(t, q + 32 * j, d + j, s + j);
     }
 }
@@ -803,13 +838,24 @@ float ora_ref_vec_dot_q8_0_q8_1(const void *wrow, const ora_block_q8_1 *xq, int 
     return total;
 }
 
-/* ------------------------------------ ggml CPU path (parity unpinned) -- */
+/* ------------------------------------------------------ ggml CPU path -- */
 /* Restatement of ggml's generic C routines quantize_row_q8_K_ref,
  * ggml_vec_dot_q4_K_q8_K, ggml_vec_dot_q6_K_q8_K, quantize_row_q8_0 and
- * ggml_vec_dot_q8_0_q8_0 (the vendored ref/llama.cpp that BASELINE names is an
- * empty directory in the reference; no version is pinned).  CPU baseline only. */
+ * ggml_vec_dot_q8_0_q8_0 (the vendored ref/llama.cpp is an empty directory in
+ * the reference; no version is pinned).  The CPU baseline, and the "no worse
+ * than the q8_K path" yardstick.  Pinned by what the mathematics fixes
+ * (tests/test_oracle.py): the dots equal the fp64 sum of the pinned
+ * dequantized weights times d q of the activation blocks, within fp32
+ * reassociation; the q8_K quantizer's closed-form properties (|q| <= 127, the
+ * argmax code -127, bsums = the 16-value code sums, |x - d q| <= |d| / 2,
+ * round half to even at constructed ties).  ORA_PLANT (0 in every normal
+ * build) plants one known mistake each for the test that shows those checks
+ * catch it. */
+#ifndef ORA_PLANT
+#define ORA_PLANT 0
+#endif
 
-static int nearest_int(float f) { return (int)lrintf(f); }  /* round half to even */
+static int nearest_int(float f) { return ORA_PLANT == 3 ? (int)roundf(f) : (int)lrintf(f); }  /* half to even */
 
 void ora_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
     ora_block_q8_K *y = (ora_block_q8_K *)vy;
@@ -826,7 +872,7 @@ void ora_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
         }
         for (int j = 0; j < 16; ++j) {
             int sum = 0;
-            for (int l = 0; l < 16; ++l) sum += y[i].qs[16 * j + l];
+            for (int l = 0; l < 16; ++l) sum += y[i].qs[(ORA_PLANT == 2 ? 8 : 16) * j + l];
             y[i].bsums[j] = (int16_t)sum;
         }
         y[i].d = 1.f / iscale;
@@ -847,10 +893,11 @@ float ora_vec_dot_q4_K_q8_K(int n, const void *vx, const void *vy) {
         uint8_t sc[8], mn[8];
         for (int j = 0; j < 8; ++j) ora_get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
         int sumi = 0;
-        for (int j = 0; j < 16; ++j) sumi += y[i].bsums[j] * mn[j / 2];
+        for (int j = 0; j < 16; ++j) sumi += y[i].bsums[j] * mn[ORA_PLANT == 1 ? j % 8 : j / 2];
         int aux32[8] = {0};
         for (int j = 0; j < 8; ++j)
-            for (int l = 0; l < 32; ++l) aux32[l % 8] += sc[j] * (a[32 * j + l] * y[i].qs[32 * j + l]);
+            for (int l = 0; l < 32; ++l)
+                aux32[l % 8] += sc[ORA_PLANT == 6 ? j ^ 1 : j] * (a[32 * j + l] * y[i].qs[32 * j + l]);
         const float d = ora_fp16_to_fp32(x[i].d) * y[i].d;
         for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
         const float dmin = ora_fp16_to_fp32(x[i].dmin) * y[i].d;
@@ -876,7 +923,8 @@ float ora_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
             }
         int aux32[8] = {0};
         for (int j = 0; j < 16; ++j)
-            for (int l = 0; l < 16; ++l) aux32[l % 8] += x[i].scales[j] * (a[16 * j + l] * y[i].qs[16 * j + l]);
+            for (int l = 0; l < 16; ++l)
+                aux32[l % 8] += x[i].scales[ORA_PLANT == 4 ? j / 2 : j] * (a[16 * j + l] * y[i].qs[16 * j + l]);
         const float d = ora_fp16_to_fp32(x[i].d) * y[i].d;
         for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
     }
@@ -900,7 +948,7 @@ float ora_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy) {
     float sumf = 0.f;
     for (int i = 0; i < n / 32; ++i) {
         int sumi = 0;
-        for (int l = 0; l < 32; ++l) sumi += x[i].qs[l] * y[i].qs[l];
+        for (int l = 0; l < 32; ++l) sumi += x[i].qs[l] * y[i].qs[ORA_PLANT == 5 ? 31 - l : l];
         sumf += (float)sumi * (ora_fp16_to_fp32(x[i].d) * ora_fp16_to_fp32(y[i].d));
     }
     return sumf;
@@ -966,7 +1014,10 @@ int ora_sample(const int32_t *idx, const float *val, int k, float temperature, f
     int kept[64];
     float sum = 0.f;
     for (int i = 0; i < k; ++i) {
-        p[i] = expf((val[i] - val[0]) / temperature);
+        /* std::exp in sample() (src/mono27b_chat.cpp:235); here the fixed exp,
+         * 0 below e^-87, NaN passed through */
+        const float a = (val[i] - val[0]) / temperature;
+        p[i] = a >= -87.0f ? ora_exp_cw(a) : (a < -87.0f ? 0.0f : a);
         sum += p[i];
     }
     if (!(sum > 0.f) || !isfinite(sum)) return idx[0];

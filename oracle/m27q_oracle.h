@@ -104,11 +104,18 @@ void ora_quantize_row_q8_0(const float *x, void *blocks, int64_t k);
 void ora_quantize_row_iq4_xs(const float *x, void *blocks, int64_t k);
 
 /* Activation format of the MI355X path: per 32 values, int8 codes, an fp32
- * scale d = amax/127 (IEEE divide), id = d != 0 ? 1/d : 0 (IEEE divide),
- * q = roundf(x * id) clamped to +-127 (ggml's quantize_row_q8_1_ref rule), and
- * the two 16-value integer code sums packed as (int16 lo) | (int16 hi) << 16. */
+ * scale d = amax/127 (IEEE divide), id = 1/d (IEEE divide) where that is
+ * finite and 0 otherwise (d == 0, or d subnormal below 2^-128), q = roundf(x *
+ * id) clamped to +-127 (ggml's quantize_row_q8_1_ref rule), and the two
+ * 16-value integer code sums packed as (int16 lo) | (int16 hi) << 16. */
 void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s);
-/* Same on x * sigmoid(g) (exec:109-138); sigmoid as 1/(1+expf(-g)). */
+/* The build's fixed exp (Cody-Waite reduction + degree-7 Taylor polynomial,
+ * argument clamped to [-87, 87]) and the gate x * (1 / (1 + e^-g)). */
+float ora_exp_cw(float t);
+float ora_gated(float x, float g);
+void ora_exp_cw_n(const float *t, float *out, size_t n);
+void ora_gated_n(const float *x, const float *g, float *out, size_t n);
+/* Same on ora_gated(x, g) (exec:109-138). */
 void ora_quant_act_gated(const float *x, const float *g, int64_t k, int8_t *q, float *d, uint32_t *s);
 
 /* Integer-dot of one weight row against the activation format, evaluated in
@@ -143,7 +150,7 @@ int ora_gemv_cpu(int type, const void *w, int rb, int rc, const void *xq, float 
 
 /* sample() (src/mono27b_chat.cpp:203-270) after its top-k, on candidates
  * idx/val in rank order: temperature <= 0 -> idx[0]; softmax at the
- * temperature (expf, float32, sums in candidate order), min_p and top_p cuts,
+ * temperature (ora_exp_cw, 0 below e^-87; float32, sums in candidate order), min_p and top_p cuts,
  * pick = u * total, the first candidate whose running sum reaches it. */
 int ora_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p, float u);
 

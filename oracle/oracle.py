@@ -45,6 +45,11 @@ def lib() -> C.CDLL:
             "ora_quantize_row_iq4_xs": (None, [P, P, I64]),
             "ora_quant_act": (None, [P, I64, P, P, P]),
             "ora_quant_act_gated": (None, [P, P, I64, P, P, P]),
+            "ora_exp_cw_n": (None, [P, P, C.c_size_t]),
+            "ora_gated_n": (None, [P, P, P, C.c_size_t]),
+            "ora_vec_dot_q4_K_q8_K": (C.c_float, [I, P, P]),
+            "ora_vec_dot_q6_K_q8_K": (C.c_float, [I, P, P]),
+            "ora_vec_dot_q8_0_q8_0": (C.c_float, [I, P, P]),
             "ora_dot_act": (D, [I, P, I, P, P, P, P]),
             "ora_gemv_act": (I, [I, P, I, I, P, P, P, P, P]),
             "ora_gemv_f64": (I, [I, P, I, I, P, P]),
@@ -158,6 +163,23 @@ def quant_act_gated(x: np.ndarray, g: np.ndarray):
     return q, d, s
 
 
+def exp_cw(t: np.ndarray) -> np.ndarray:
+    """The build's fixed exp (ora_exp_cw), elementwise on float32."""
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    out = np.empty(t.shape, np.float32)
+    lib().ora_exp_cw_n(_p(t), _p(out), t.size)
+    return out
+
+
+def gated(x: np.ndarray, g: np.ndarray) -> np.ndarray:
+    """x * (1 / (1 + e^-g)) with the fixed exp (ora_gated), elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().ora_gated_n(_p(x), _p(g), _p(out), x.size)
+    return out
+
+
 def gemv_act(type_: int, blocks: np.ndarray, rb: int, rc: int, q, d, s):
     """Integer-dot oracle in fp64; returns (y, norm) each float64 [rc]."""
     blocks = np.ascontiguousarray(blocks)
@@ -208,6 +230,30 @@ def quant_cpu_act(type_: int, x: np.ndarray) -> np.ndarray:
         out = np.empty(x.size // 256 * 292, np.uint8)
         lib().ora_quantize_row_q8_K(_p(x), _p(out), x.size)
     return out
+
+
+Q8_K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
+Q8_0_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
+
+
+def cpu_act_values(type_: int, xq: np.ndarray) -> np.ndarray:
+    """The activation a q8_K / q8_0 buffer stands for, d * q, in float64."""
+    if type_ == Q8_0:
+        b = np.frombuffer(np.ascontiguousarray(xq).tobytes(), Q8_0_DTYPE)
+        d = fp16_to_fp32(b["d"]).astype(np.float64)
+    else:
+        b = np.frombuffer(np.ascontiguousarray(xq).tobytes(), Q8_K_DTYPE)
+        d = b["d"].astype(np.float64)
+    return (d[:, None] * b["qs"].astype(np.float64)).reshape(-1)
+
+
+def vec_dot_cpu(type_: int, wrow: np.ndarray, xq: np.ndarray, n: int) -> float:
+    """One row of ggml_vec_dot_{q4_K_q8_K, q6_K_q8_K, q8_0_q8_0} (restated)."""
+    fn = {Q4_K: lib().ora_vec_dot_q4_K_q8_K, Q6_K: lib().ora_vec_dot_q6_K_q8_K,
+          Q8_0: lib().ora_vec_dot_q8_0_q8_0}[type_]
+    wrow = np.ascontiguousarray(wrow)
+    xq = np.ascontiguousarray(xq)
+    return float(fn(n, _p(wrow), _p(xq)))
 
 
 def gemv_cpu(type_: int, blocks: np.ndarray, rb: int, rc: int, xq: np.ndarray, nthreads: int = 1) -> np.ndarray:

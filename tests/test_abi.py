@@ -141,8 +141,16 @@ def test_validation_multi_and_swiglu(m27q):
     assert L.m27q_matvec_q8_multi(2, ws, FAKE, ys, None) == 2       # row_blocks differ
     assert L.m27q_matvec_q8_multi(0, ws, FAKE, ys, None) == 2
     assert L.m27q_matvec_q8_multi(5, ws, FAKE, ys, None) == 2
-    ws2 = (m27q.WeightDesc * 2)(W(m27q), W(m27q, t=m27q.Q6_K))
-    assert L.m27q_matvec_q8_multi(2, ws2, FAKE, ys, None) == 3
+    # types may differ (one launch per type) but K may not: Q8_0 with 20 blocks is K = 640
+    ws2 = (m27q.WeightDesc * 2)(W(m27q), W(m27q, t=m27q.Q8_0))
+    assert L.m27q_matvec_q8_multi(2, ws2, FAKE, ys, None) == 2
+    assert L.m27q_matvec_multi(2, ws2, FAKE, ys, None) == 2
+    # every member is checked before the first launch: a bad second-type member stops both
+    ws4 = (m27q.WeightDesc * 2)(W(m27q), W(m27q, t=m27q.Q6_K, ptr=0))
+    assert L.m27q_matvec_q8_multi(2, ws4, FAKE, ys, None) == 1
+    ws5 = (m27q.WeightDesc * 2)(W(m27q), W(m27q, t=m27q.Q6_K, layout=m27q.GGUF, ptr=FAKE + 1))
+    assert L.m27q_matvec_q8_multi(2, ws5, FAKE, ys, None) == 4
+    assert L.m27q_matmul_q8_multi(2, ws2, 4, FAKE, ys, None) == 2
     ys0 = (C.c_void_p * 2)(FAKE, None)
     ws3 = (m27q.WeightDesc * 2)(W(m27q), W(m27q))
     assert L.m27q_matvec_q8_multi(2, ws3, FAKE, ys0, None) == 1

@@ -116,3 +116,71 @@ def test_retile_blob_errors(m27q, ref, tmp_path):
     assert L.m27q_retile_blob(str(tmp_path / "missing").encode(), str(tmp_path / "y").encode()) == 8
     assert L.m27q_retile_blob(p.encode(), p.encode()) == 8
     assert L.m27q_retile_blob(None, p.encode()) == 1
+
+
+def test_blob_tensors_match_the_reference_reader(m27q, ref, tmp_path):
+    """m27q_blob_tensors on a re-tiled blob gives the entries the reference's
+    mono27b_read_weights_section reads, with the layout from the reserved
+    field, WeightView's row_blocks and absolute file offsets."""
+    src, dst = str(tmp_path / "in.m27b"), str(tmp_path / "out.m27b")
+    write_blob(ref, m27q, src, np.random.default_rng(9))
+    m27q.retile_blob(src, dst)
+    for path in (src, dst):
+        want = read_entries(ref, path)
+        got = m27q.blob_tensors(path)
+        base = ref.refblob_weights_offset(path.encode())
+        assert len(got) == len(want)
+        for g, w, (name, t, role, re, rc) in zip(got, want, TENSORS):
+            assert g.name == w["name"] and g.ggml_type == w["ggml_type"] and g.role == w["role"]
+            assert g.source_model == w["source_model"] and g.row_elems == re and g.row_count == rc
+            assert g.layout == w["reserved"] and g.bytes == w["data_bytes"]
+            assert g.file_offset == base + int(w["data_offset"])
+            assert g.row_blocks == re // m27q.BLOCK_ELEMS[t]
+            assert g.bytes == m27q.weight_bytes(t, g.row_blocks, rc, g.layout)
+
+
+ENTRY_OFF_DATA_OFFSET, ENTRY_OFF_DATA_BYTES = 88, 96
+
+
+def _patch_entry(path, ref, i, field_off, value):
+    base = ref.refblob_weights_offset(path.encode())
+    with open(path, "r+b") as f:
+        f.seek(base + 16 + i * ENTRY.itemsize + field_off)
+        f.write(int(value).to_bytes(8, "little"))
+
+
+@pytest.mark.parametrize("field_off,value", [
+    (ENTRY_OFF_DATA_OFFSET, 2 ** 64 - 8),     # offset + bytes wraps around
+    (ENTRY_OFF_DATA_BYTES, 2 ** 64 - 1),      # bytes alone wraps
+    (ENTRY_OFF_DATA_OFFSET, 1 << 40),         # past the section
+])
+def test_blob_readers_reject_out_of_range_entries(m27q, ref, tmp_path, field_off, value):
+    src = str(tmp_path / "in.m27b")
+    write_blob(ref, m27q, src, np.random.default_rng(10))
+    _patch_entry(src, ref, 2, field_off, value)
+    L = m27q.lib()
+    n = C.c_int(0)
+    assert L.m27q_blob_tensors(src.encode(), None, 0, C.byref(n)) == 8
+    assert L.m27q_retile_blob(src.encode(), str(tmp_path / "o.m27b").encode()) == 8
+
+
+def test_blob_load_checks_before_any_copy(m27q, ref, tmp_path):
+    """m27q_blob_load validates the record and the destination size on the host
+    and returns before any HIP call (no GPU needed for these)."""
+    src = str(tmp_path / "in.m27b")
+    write_blob(ref, m27q, src, np.random.default_rng(12))
+    ts = m27q.blob_tensors(src)
+    L = m27q.lib()
+    w = m27q.WeightDesc()
+    fake = 1 << 20  # never dereferenced: every case below fails its host check first
+    t = m27q.BlobTensor.from_buffer_copy(ts[0])
+    assert L.m27q_blob_load(src.encode(), C.byref(t), fake, int(t.bytes) - 1, C.byref(w)) == 2
+    t.layout = 7
+    assert L.m27q_blob_load(src.encode(), C.byref(t), fake, int(t.bytes), C.byref(w)) == 4
+    t = m27q.BlobTensor.from_buffer_copy(ts[0])
+    t.row_blocks = 0
+    assert L.m27q_blob_load(src.encode(), C.byref(t), fake, int(t.bytes), C.byref(w)) == 3
+    t = m27q.BlobTensor.from_buffer_copy(ts[0])
+    t.bytes += 1
+    assert L.m27q_blob_load(src.encode(), C.byref(t), fake, int(t.bytes), C.byref(w)) == 2
+    assert L.m27q_blob_load(src.encode(), C.byref(ts[0]), None, 10 ** 9, C.byref(w)) == 1

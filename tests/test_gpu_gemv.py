@@ -377,3 +377,40 @@ def test_properties_full_size(m27q, ora, dev, type_name, rc, k):
         col = to_host(deq)[:, j % 256].astype(np.float64)
         got = to_host(y).astype(np.float64)
         assert np.allclose(got, 127.0 * col, rtol=1e-6, atol=1e-6 * np.abs(127.0 * col).max())
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_mixed_type_pair_ssm_shapes(m27q, ora, dev, layout):
+    """l_mv_pair's SSM-layer pair (exec:2106-2125, :2492): wqkv Q6_K 10240 x 5120
+    and wqkv_gate Q5_K 6144 x 5120 on one activation, through the multi entry
+    points (one launch per type); each output matches the integer-dot oracle
+    and is bit-identical to the single product on the same activation."""
+    import torch
+    k = 5120
+    spec = [("Q6_K", 10240, 31), ("Q5_K", 6144, 32)]
+    ws, bl = [], []
+    for name, rc, seed in spec:
+        t = getattr(m27q, name)
+        wb = weights(ora, name, rc, k, seed)
+        bl.append(wb)
+        ws.append(m27q.Weight.upload(wb.reshape(-1), t, k // 256, rc, layout, dev))
+    x, act = quantized_x(m27q, dev, k, 33)
+    q, d, s = act_host(m27q, act)
+    xd = to_dev(x, dev)
+    for form in ("q8", "fp32"):
+        ys = [torch.empty(rc, dtype=torch.float32, device=dev) for _, rc, _ in spec]
+        one = [torch.empty(rc, dtype=torch.float32, device=dev) for _, rc, _ in spec]
+        say("mixed pair", form, "layout", layout)
+        if form == "q8":
+            m27q.matvec_q8_multi(ws, act, ys)
+            for w, y in zip(ws, one):
+                m27q.matvec_q8(w, act, y)
+        else:
+            m27q.matvec_multi(ws, xd, ys)
+            for w, y in zip(ws, one):
+                m27q.matvec(w, xd, y)
+        for (name, rc, _), w, wb, y, y1 in zip(spec, ws, bl, ys, one):
+            got = to_host(y)
+            want, nrm = ora.gemv_act(w.type, wb, w.rb, rc, q[0], d[0], s[0])
+            assert (np.abs(got.astype(np.float64) - want) <= int_dot_tol(nrm)).all(), (form, name)
+            assert np.array_equal(got.view(np.uint32), to_host(y1).view(np.uint32)), (form, name)

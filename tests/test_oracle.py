@@ -334,3 +334,164 @@ def test_sample_properties(ora):
         for i, want in zip(ks, q):
             assert abs((got == idx[i]).mean() - want) <= 2.0 / N + 1e-6
         assert set(got) <= set(idx[ks])
+
+
+# ------------------------------------------ the fixed exp and the gate --
+
+def _ulps(got, want64):
+    """|got - want| in units of the float32 spacing at want."""
+    w32 = want64.astype(np.float32)
+    return np.abs(got.astype(np.float64) - want64) / np.spacing(np.abs(w32)).astype(np.float64)
+
+
+def test_exp_cw_within_2_ulp(ora):
+    """ora_exp_cw (Cody-Waite reduction + degree-7 Taylor polynomial) against
+    float64 exp: every 97th float in [-87, 87], plus the clamp ends."""
+    lo = np.float32(-87.0).view(np.uint32)
+    hi = np.float32(87.0).view(np.uint32)
+    pos = np.arange(0, int(hi) + 1, 97, dtype=np.uint32).view(np.float32)
+    neg = np.arange(0x80000000, int(lo) + 1, 97, dtype=np.uint32).view(np.float32)
+    t = np.concatenate([pos, neg, np.float32([87.0, -87.0, 0.5, -0.5, 1e-30, -1e-30])])
+    got = ora.exp_cw(t)
+    assert np.all(np.isfinite(got)) and np.all(got > 0)
+    assert _ulps(got, np.exp(t.astype(np.float64))).max() <= 2.0
+    assert ora.exp_cw(np.float32([0.0, -0.0]))[0] == 1.0
+    ends = ora.exp_cw(np.float32([-1e4, -88.0, np.nan, -np.inf, 1e4, 88.0, np.inf]))
+    e_lo, e_hi = ora.exp_cw(np.float32([-87.0, 87.0]))
+    assert np.array_equal(ends, np.float32([e_lo] * 4 + [e_hi] * 3))
+    # monotone over a fine sorted sweep (an off coefficient would show as a step)
+    s = np.sort(t)
+    assert np.all(np.diff(ora.exp_cw(s).astype(np.float64)) >= 0)
+
+
+def test_gated_against_float64_sigmoid(ora):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(200000) * 10.0 ** rng.integers(-3, 4, 200000)).astype(np.float32)
+    g = (rng.standard_normal(200000) * 8).astype(np.float32)
+    got = ora.gated(x, g).astype(np.float64)
+    want = x.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    # exp within 2 ulp, then an add, a divide and a multiply: a few ulp at most
+    assert (np.abs(got - want) <= 8 * 2.0 ** -24 * np.abs(want) + 1e-45).all()
+    # saturation: the gate is 1 far to the right, and x e^-87 / (1 + ...) far to the left
+    assert np.array_equal(ora.gated(np.float32([3.0, -2.0]), np.float32([40.0, 1e4])), np.float32([3.0, -2.0]))
+    far = ora.gated(np.float32([1.0]), np.float32([-1e4]))[0]
+    assert 0 < far <= np.float32(1.7e-38)
+
+
+def test_quant_act_subnormal_scale_groups(ora):
+    """A group whose 1/d is not finite (d subnormal below 2^-128) gets all-zero
+    codes and keeps its d; a subnormal d with a finite 1/d quantizes normally."""
+    x = np.zeros(96, np.float32)
+    x[0:32] = np.float32(1e-40) * np.arange(1, 33, dtype=np.float32)   # amax 3.2e-39: 1/d inf
+    x[32:64] = np.float32(5e-37) * np.linspace(-1, 1, 32, dtype=np.float32)  # d ~ 3.9e-39: 1/d finite
+    x[64:96] = RNG.standard_normal(32).astype(np.float32)
+    q, d, s = ora.quant_act(x)
+    assert d[0] == np.float32(np.float32(3.2e-39) / np.float32(127)) and d[0] > 0
+    assert (q[0:32] == 0).all() and s[0] == 0
+    assert np.isfinite(np.float32(1) / d[1])
+    assert q[32] == -127 and q[63] == 127
+    q2, d2, _ = ora.quant_act(x[64:96].copy())
+    assert np.array_equal(q[64:96], q2) and d[2] == d2[0]
+
+
+# ------------------------------ ggml CPU path (q8_K / q8_0): the pins --
+
+def _oracle_variant(plant, tmp):
+    """The oracle built with ORA_PLANT = plant (one planted mistake), as ctypes."""
+    import ctypes as C
+    import subprocess
+    src = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "m27q_oracle.c")
+    so = os.path.join(tmp, f"libora_plant{plant}.so")
+    subprocess.run(["gcc", "-O2", "-march=x86-64-v3", "-ffp-contract=off", "-fPIC", "-std=c11", "-pthread",
+                    "-shared", f"-DORA_PLANT={plant}", "-o", so, src, "-lm"], check=True)
+    return C.CDLL(so)
+
+
+def q8k_pin_failures(ora, L):
+    """Names of the checks that the ggml-path routines of library L fail:
+    the quantize_row_q8_K properties fixed by its definition, and each vec-dot
+    against the fp64 sum of the pinned dequantized weights times the values
+    (d q) its activation blocks stand for."""
+    import ctypes as C
+    P = C.c_void_p
+    L.ora_quantize_row_q8_K.argtypes = [P, P, C.c_int64]
+    L.ora_quantize_row_q8_0_act.argtypes = [P, P, C.c_int64]
+    for f in ("ora_vec_dot_q4_K_q8_K", "ora_vec_dot_q6_K_q8_K", "ora_vec_dot_q8_0_q8_0"):
+        getattr(L, f).argtypes = [C.c_int, P, P]
+        getattr(L, f).restype = C.c_float
+
+    def q8k(x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 256 * 292, np.uint8)
+        L.ora_quantize_row_q8_K(x.ctypes.data, out.ctypes.data, x.size)
+        return out
+
+    fails = []
+    rng = np.random.default_rng(77)
+    x = (rng.standard_normal(4096) * 3).astype(np.float32)
+    x[256:512] = 0.0
+    b = np.frombuffer(q8k(x).tobytes(), ora.Q8_K_DTYPE)
+    q = b["qs"].astype(np.int64)
+    d = b["d"].astype(np.float64)
+    xb = x.reshape(-1, 256)
+    live = np.abs(xb).max(1) > 0
+    if np.abs(q).max() > 127:
+        fails.append("q8_K codes within +-127")
+    am = np.abs(xb).argmax(1)
+    if not (q[live, am[live]] == -127).all():
+        fails.append("q8_K argmax code -127")
+    if not np.array_equal(b["bsums"].astype(np.int64), q.reshape(-1, 16, 16).sum(-1)):
+        fails.append("q8_K bsums are the 16-value code sums")
+    if not (np.abs(xb[live] - d[live, None] * q[live]) <= np.abs(d[live, None]) * (0.5 + 2.0 ** -16)).all():
+        fails.append("q8_K |x - d q| <= |d| / 2")
+    if not ((q[~live] == 0).all() and (d[~live] == 0).all()):
+        fails.append("q8_K zero block")
+    t = np.zeros(256, np.float32)
+    t[0] = -127.0  # iscale = -127 / vmax = 1 exactly
+    t[1:8] = [2.5, 3.5, -2.5, 0.5, -0.5, 1.5, 126.5]
+    bt = np.frombuffer(q8k(t).tobytes(), ora.Q8_K_DTYPE)[0]
+    if list(bt["qs"][:8]) != [-127, 2, 4, -2, 0, 0, 2, 126] or bt["d"] != 1.0:
+        fails.append("q8_K round half to even")
+
+    K, rc = 2048, 24
+    xs = rng.standard_normal(K).astype(np.float32)
+    for t_ in (ora.Q4_K, ora.Q6_K, ora.Q8_0):
+        rb = K // ora.BLOCK_ELEMS[t_]
+        w = ora.synth_weights(t_, rc, K, seed=40 + t_)
+        if t_ == ora.Q8_0:
+            xq = np.zeros(K // 32 * 34, np.uint8)
+            L.ora_quantize_row_q8_0_act(xs.ctypes.data, xq.ctypes.data, K)
+        else:
+            xq = q8k(xs)
+        xv = ora.cpu_act_values(t_, xq)
+        W = ora.dequant(t_, w, rb, rc).astype(np.float64)
+        want = W @ xv
+        nrm = np.abs(W) @ np.abs(xv)
+        if t_ == ora.Q4_K:  # the d sc q and dmin m terms separately: zero the quants
+            w0 = w.reshape(rc, rb, 144).copy()
+            w0[:, :, 16:] = 0
+            nrm = nrm + 2 * np.abs(ora.dequant(t_, w0.reshape(rc, -1), rb, rc).astype(np.float64)) @ np.abs(xv)
+        fn = {ora.Q4_K: L.ora_vec_dot_q4_K_q8_K, ora.Q6_K: L.ora_vec_dot_q6_K_q8_K,
+              ora.Q8_0: L.ora_vec_dot_q8_0_q8_0}[t_]
+        got = np.array([fn(K, np.ascontiguousarray(w[r]).ctypes.data, xq.ctypes.data) for r in range(rc)])
+        if not (np.abs(got - want) <= K * 2.0 ** -24 * nrm).all():
+            fails.append(f"vec_dot type {t_} = sum dequant(W) d q")
+    return fails
+
+
+def test_q8k_cpu_path_pinned(ora):
+    """ggml's q8_K / q8_0 CPU path as restated: every pin holds."""
+    assert q8k_pin_failures(ora, ora.lib()) == []
+
+
+@pytest.mark.parametrize("plant,check", [
+    (1, "vec_dot type 12"),           # min paired with the wrong bsums
+    (2, "bsums"),                     # bsums over the wrong 16 codes
+    (3, "half to even"),              # q8_K rounds half away from zero
+    (4, "vec_dot type 14"),           # Q6_K scale of the wrong 16-group
+    (5, "vec_dot type 8"),            # Q8_0 codes paired in the wrong order
+    (6, "vec_dot type 12"),           # Q4_K scale of the neighbouring group
+])
+def test_q8k_pins_catch_planted_mistakes(ora, tmp_path, plant, check):
+    fails = q8k_pin_failures(ora, _oracle_variant(plant, str(tmp_path)))
+    assert any(check in f for f in fails), fails
