@@ -89,6 +89,17 @@ STAGES = {
 }
 STAGE_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
 
+# Config 4: the same products on M quantized activation rows (A[K] holds the M
+# rows of length K; Y[name] is [M][rows]).
+STAGES_M = {
+    "qkv": lambda m27q, L, A, Y, s: m27q.matmul_q8_multi([L["q"], L["k"], L["v"]], A[5120], [Y["q"], Y["k"], Y["v"]],
+                                                         stream=s),
+    "o": lambda m27q, L, A, Y, s: m27q.matmul_q8(L["o"], A[6144], Y["o"], stream=s),
+    "gate_up": lambda m27q, L, A, Y, s: m27q.matmul_q8_multi([L["gate"], L["up"]], A[5120], [Y["gate"], Y["up"]],
+                                                             stream=s),
+    "down": lambda m27q, L, A, Y, s: m27q.matmul_q8(L["down"], A[17408], Y["down"], stream=s),
+}
+
 
 def stage_bytes(m27q, name):
     """Algorithmic HBM bytes of one product: GGUF weight bytes (unpadded) + fp32
@@ -185,11 +196,8 @@ def suite(m27q, torch, dev, layers, reps):
         Ys = {n: torch.empty((M, rc), dtype=torch.float32, device=dev) for n, _, rc, _ in LAYER}
 
         def layer_m(c, st):
-            L = layers[c]
-            m27q.matmul_q8_multi([L["q"], L["k"], L["v"]], acts[5120], [Ys["q"], Ys["k"], Ys["v"]], stream=st)
-            m27q.matmul_q8(L["o"], acts[6144], Ys["o"], stream=st)
-            m27q.matmul_q8_multi([L["gate"], L["up"]], acts[5120], [Ys["gate"], Ys["up"]], stream=st)
-            m27q.matmul_q8(L["down"], acts[17408], Ys["down"], stream=st)
+            for fn in STAGES_M.values():
+                fn(m27q, layers[c], acts, Ys, st)
         us = timed(torch, layer_m, len(layers), reps)
         lb = sum(m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256 for _, t, rc, k in LAYER)
         out[f"cfg4_layer_m{M}"] = {"us": round(us, 3), "GBps": round(lb / us / 1e3, 1)}
