@@ -300,6 +300,19 @@ M27Q_API size_t m27q_topk_scratch_bytes(int n, int k);
 M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, float *val, void *scratch,
                                size_t scratch_bytes, hipStream_t stream);
 
+/* m27q_topk without a scratch argument: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The library keeps the
+ * scratch in a static device array of m27q_topk_scratch_bytes (133,128 bytes;
+ * n <= 2^24) per device, held until the process ends; n beyond that returns
+ * M27Q_ERR_SCRATCH before any launch.  The first call on a device resolves
+ * the array's address (hipGetSymbolAddress), so make it outside graph
+ * capture.  Every call on a device shares that device's array: calls that
+ * overlap on one device (two streams, two threads) race.  Nothing here
+ * allocates or frees. */
+M27Q_API m27q_status m27q_topk_noalloc(const float *logits, int n, int k, int32_t *idx, float *val,
+                                       hipStream_t stream);
+
 /* On-device token choice from m27q_topk's candidates (idx/val in rank order,
  * 1 <= k <= 64), the steps of sample() (src/mono27b_chat.cpp:203-270) after its
  * top-k: temperature <= 0 gives idx[0] (the argmax, first index on ties);

@@ -480,6 +480,18 @@ M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, 
     return hip_status(launch_topk(logits, n, k, idx, val, scratch, stream));
 }
 
+M27Q_API m27q_status m27q_topk_noalloc(const float *logits, int n, int k, int32_t *idx, float *val,
+                                       hipStream_t stream) {
+    if (!logits || !idx || !val) return M27Q_ERR_NULL;
+    if (n <= 0) return M27Q_ERR_SHAPE;
+    if (k < 1 || k > kMaxTopK || k > n) return M27Q_ERR_RANGE;
+    const size_t need = topk_scratch_bytes(n);
+    if (need == 0 || need > topk_static_scratch_bytes()) return M27Q_ERR_SCRATCH;
+    void *scratch = nullptr;
+    if (topk_static_scratch(&scratch) != hipSuccess) return M27Q_ERR_HIP;
+    return hip_status(launch_topk(logits, n, k, idx, val, scratch, stream));
+}
+
 M27Q_API m27q_status m27q_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p,
                                  float top_p, const float *u, int32_t *token, hipStream_t stream) {
     if (!idx || !val || !u || !token) return M27Q_ERR_NULL;

@@ -65,6 +65,10 @@ struct GatherParams {
 hipError_t launch_gather(const GatherParams &p, hipStream_t s);
 
 size_t topk_scratch_bytes(int n);
+// The top-k scratch array of m27q_topk.hip (static, per device): its size, and
+// its device address on the current device (resolved on the first call there).
+size_t topk_static_scratch_bytes();
+hipError_t topk_static_scratch(void **ptr);
 hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, void *scratch, hipStream_t s);
 hipError_t launch_sample(const int32_t *idx, const float *val, int k, float temperature, float min_p, float top_p,
                          const float *u, int32_t *token, hipStream_t s);

@@ -21,6 +21,8 @@
 //      select runs over the candidates.
 // Replaces the CPU selection of sample() (src/mono27b_chat.cpp:211-227) and
 // k_argmax (exec:211-239).
+#include <atomic>
+
 #include "m27q_internal.h"
 #include "m27q_device.h"
 
@@ -389,6 +391,36 @@ int topk_max_n() { return (1 << 16) * kTopkMaxChunks; }
 size_t topk_scratch_bytes(int n) {
     if (!topk_chunk(n)) return 0;
     return (size_t)(kTopkMaxChunks + 1 + kTopkCap) * sizeof(uint64_t);
+}
+
+// The library's own top-k scratch for callers that cannot allocate
+// (m27q_topk_noalloc): one fixed-size array per device, held until the
+// process ends.  Host code never passes the array's name to a kernel: its
+// device address is resolved once per device with hipGetSymbolAddress and
+// cached.  Every call on a device shares that device's array (k_topk_chunk_max
+// clears the candidate counter in the array itself on every call), so calls
+// that overlap on one device race.
+constexpr size_t kTopkScratchWords = (size_t)kTopkMaxChunks + 1 + kTopkCap;
+static __device__ __align__(256) uint64_t scratch[kTopkScratchWords];
+
+size_t topk_static_scratch_bytes() { return sizeof(scratch); }
+
+hipError_t topk_static_scratch(void **ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<void *> cache[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    void *p = cache[dev].load(std::memory_order_acquire);
+    if (!p) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        cache[dev].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return hipSuccess;
 }
 
 hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, void *scratch, hipStream_t s) {

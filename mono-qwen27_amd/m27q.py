@@ -74,6 +74,7 @@ _SIGS = {
     "m27q_embed_token": (_I, [C.POINTER(WeightDesc), C.c_int32, _P, _P]),
     "m27q_topk_scratch_bytes": (_SZ, [_I, _I]),
     "m27q_topk": (_I, [_P, _I, _I, _P, _P, _P, _SZ, _P]),
+    "m27q_topk_noalloc": (_I, [_P, _I, _I, _P, _P, _P]),
     "m27q_sample": (_I, [_P, _P, _I, C.c_float, C.c_float, C.c_float, _P, _P, _P]),
 }
 
@@ -322,3 +323,9 @@ def topk(logits, k: int, idx, val, scratch, stream=None) -> None:
     n = logits.numel()
     check(lib().m27q_topk(_ptr(logits), n, k, _ptr(idx), _ptr(val), _ptr(scratch),
                           scratch.numel() * scratch.element_size(), _stream(stream)), "m27q_topk")
+
+
+def topk_noalloc(logits, k: int, idx, val, stream=None) -> None:
+    """m27q_topk on the library's static scratch (no scratch argument)."""
+    check(lib().m27q_topk_noalloc(_ptr(logits), logits.numel(), k, _ptr(idx), _ptr(val), _stream(stream)),
+          "m27q_topk_noalloc")
