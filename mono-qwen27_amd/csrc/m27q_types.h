@@ -254,8 +254,9 @@ struct Q6K {
 
     struct Frag {
         uint4 ql, qh;
-        uint2 sc;    // scales[8hh .. 8hh+8)
-        uint32_t d;  // f16 bits
+        uint2 sc;      // scales[8hh .. 8hh+8)
+        uint32_t d;    // f16 bits of d at bit dsh
+        uint32_t dsh;  // 0 or 16
     };
 
     struct Lane {
@@ -279,7 +280,8 @@ struct Q6K {
         f.ql = ld_u128(unit + kQ6KTQl + 128 * i + 16 * c);
         f.qh = ld_u128(unit + kQ6KTQh + 64 * i + L.qh_off);
         f.sc = *(const uint2 *)(unit + kQ6KTSc + 16 * i + 8 * L.hh);
-        f.d = *(const uint16_t *)(unit + kQ6KTD + 2 * i);
+        f.d = *(const uint32_t *)(unit + kQ6KTD + 4 * (i >> 1));  // the d pair of rows i & ~1, i | 1
+        f.dsh = 16 * (i & 1);
         return f;
     }
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &L) {
@@ -289,6 +291,7 @@ struct Q6K {
         f.qh = ld_u128_a2(blk + kQ6KQh + L.qh_off);
         f.sc = make_uint2(ld_u32_a2(blk + kQ6KSc + 8 * L.hh), ld_u32_a2(blk + kQ6KSc + 8 * L.hh + 4));
         f.d = *(const uint16_t *)(blk + kQ6KD);
+        f.dsh = 0;
         return f;
     }
 
@@ -347,7 +350,7 @@ struct Q6K {
         const int schi = (int)(int8_t)(f.sc.y >> (8 * L.cc));
         // |sums| <= 32 * 127 * 16 < 2^23 and |scales| <= 128: exact 24-bit products.
         const float t = fmaf(a.dhi, (float)__mul24(shi, schi), a.dlo * (float)__mul24(slo, sclo));
-        return f16_bits_to_f32(f.d) * t;
+        return f16_bits_to_f32(f.d >> f.dsh) * t;
     }
     __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
         return dot(f, load_act(a, u, L), L);
@@ -372,7 +375,7 @@ struct Q6K {
         fhi -= 32.f * a.x16[g16 + 4];
         const float sclo = (float)(int8_t)(f.sc.x >> (8 * L.cc));
         const float schi = (float)(int8_t)(f.sc.y >> (8 * L.cc));
-        return f16_bits_to_f32(f.d) * (sclo * flo + schi * fhi);
+        return f16_bits_to_f32(f.d >> f.dsh) * (sclo * flo + schi * fhi);
     }
 };
 

@@ -147,6 +147,12 @@ float ora_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy);
 /* y[r] for r in [0, rc), rows split over nthreads pthreads.  xq is the
  * activation quantized to q8_K (K-quants) or q8_0 (Q8_0). */
 int ora_gemv_cpu(int type, const void *w, int rb, int rc, const void *xq, float *y, int nthreads);
+/* The same dots and row split in AVX2 (m27q_cpu_simd.c): the CPU baseline's
+ * SIMD build. */
+float ora_simd_vec_dot_q4_K_q8_K(int n, const void *vx, const void *vy);
+float ora_simd_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy);
+float ora_simd_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy);
+int ora_gemv_cpu_simd(int type, const void *w, int rb, int rc, const void *xq, float *y, int nthreads);
 
 /* sample() (src/mono27b_chat.cpp:203-270) after its top-k, on candidates
  * idx/val in rank order: temperature <= 0 -> idx[0]; softmax at the

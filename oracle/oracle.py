@@ -63,6 +63,10 @@ def lib() -> C.CDLL:
             "ora_sample": (I, [P, P, I, C.c_float, C.c_float, C.c_float, C.c_float]),
             "ora_quantize_row_q8_0_act": (None, [P, P, I64]),
             "ora_gemv_cpu": (I, [I, P, I, I, P, P, I]),
+            "ora_gemv_cpu_simd": (I, [I, P, I, I, P, P, I]),
+            "ora_simd_vec_dot_q4_K_q8_K": (C.c_float, [I, P, P]),
+            "ora_simd_vec_dot_q6_K_q8_K": (C.c_float, [I, P, P]),
+            "ora_simd_vec_dot_q8_0_q8_0": (C.c_float, [I, P, P]),
             "ora_topk": (I, [P, I, I, P, P]),
         }
         for name, (res, args) in sig.items():
@@ -256,10 +260,13 @@ def vec_dot_cpu(type_: int, wrow: np.ndarray, xq: np.ndarray, n: int) -> float:
     return float(fn(n, _p(wrow), _p(xq)))
 
 
-def gemv_cpu(type_: int, blocks: np.ndarray, rb: int, rc: int, xq: np.ndarray, nthreads: int = 1) -> np.ndarray:
+def gemv_cpu(type_: int, blocks: np.ndarray, rb: int, rc: int, xq: np.ndarray, nthreads: int = 1,
+             simd: bool = False) -> np.ndarray:
+    """ggml's CPU path as restated: scalar C, or the AVX2 build (simd)."""
     blocks = np.ascontiguousarray(blocks)
     y = np.empty(rc, np.float32)
-    assert lib().ora_gemv_cpu(type_, _p(blocks), rb, rc, _p(xq), _p(y), nthreads) == 0
+    fn = lib().ora_gemv_cpu_simd if simd else lib().ora_gemv_cpu
+    assert fn(type_, _p(blocks), rb, rc, _p(xq), _p(y), nthreads) == 0
     return y
 
 

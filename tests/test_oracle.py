@@ -407,7 +407,7 @@ def _oracle_variant(plant, tmp):
     return C.CDLL(so)
 
 
-def q8k_pin_failures(ora, L):
+def q8k_pin_failures(ora, L, dots="ora_vec_dot"):
     """Names of the checks that the ggml-path routines of library L fail:
     the quantize_row_q8_K properties fixed by its definition, and each vec-dot
     against the fp64 sum of the pinned dequantized weights times the values
@@ -416,9 +416,9 @@ def q8k_pin_failures(ora, L):
     P = C.c_void_p
     L.ora_quantize_row_q8_K.argtypes = [P, P, C.c_int64]
     L.ora_quantize_row_q8_0_act.argtypes = [P, P, C.c_int64]
-    for f in ("ora_vec_dot_q4_K_q8_K", "ora_vec_dot_q6_K_q8_K", "ora_vec_dot_q8_0_q8_0"):
-        getattr(L, f).argtypes = [C.c_int, P, P]
-        getattr(L, f).restype = C.c_float
+    for f in ("q4_K_q8_K", "q6_K_q8_K", "q8_0_q8_0"):
+        getattr(L, f"{dots}_{f}").argtypes = [C.c_int, P, P]
+        getattr(L, f"{dots}_{f}").restype = C.c_float
 
     def q8k(x):
         x = np.ascontiguousarray(x, np.float32)
@@ -471,8 +471,7 @@ def q8k_pin_failures(ora, L):
             w0 = w.reshape(rc, rb, 144).copy()
             w0[:, :, 16:] = 0
             nrm = nrm + 2 * np.abs(ora.dequant(t_, w0.reshape(rc, -1), rb, rc).astype(np.float64)) @ np.abs(xv)
-        fn = {ora.Q4_K: L.ora_vec_dot_q4_K_q8_K, ora.Q6_K: L.ora_vec_dot_q6_K_q8_K,
-              ora.Q8_0: L.ora_vec_dot_q8_0_q8_0}[t_]
+        fn = getattr(L, f"{dots}_" + {ora.Q4_K: "q4_K_q8_K", ora.Q6_K: "q6_K_q8_K", ora.Q8_0: "q8_0_q8_0"}[t_])
         got = np.array([fn(K, np.ascontiguousarray(w[r]).ctypes.data, xq.ctypes.data) for r in range(rc)])
         if not (np.abs(got - want) <= K * 2.0 ** -24 * nrm).all():
             fails.append(f"vec_dot type {t_} = sum dequant(W) d q")
@@ -482,6 +481,24 @@ def q8k_pin_failures(ora, L):
 def test_q8k_cpu_path_pinned(ora):
     """ggml's q8_K / q8_0 CPU path as restated: every pin holds."""
     assert q8k_pin_failures(ora, ora.lib()) == []
+
+
+def test_q8k_cpu_path_avx2_build_pinned(ora):
+    """The AVX2 build of the same dots (the CPU baseline's SIMD leg) meets the
+    same pins, and its rows equal the scalar restatement's within fp32
+    reassociation."""
+    assert q8k_pin_failures(ora, ora.lib(), dots="ora_simd_vec_dot") == []
+    for t in (ora.Q4_K, ora.Q6_K, ora.Q8_0):
+        k, rc = 5120, 64
+        w = ora.synth_weights(t, rc, k, seed=9)
+        x = RNG.standard_normal(k).astype(np.float32)
+        xq = ora.quant_cpu_act(t, x)
+        rb = k // ora.BLOCK_ELEMS[t]
+        a = ora.gemv_cpu(t, w, rb, rc, xq, nthreads=3)
+        b = ora.gemv_cpu(t, w, rb, rc, xq, nthreads=2, simd=True)
+        W = np.abs(ora.dequant(t, w, rb, rc).astype(np.float64))
+        nrm = W @ np.abs(ora.cpu_act_values(t, xq))
+        assert (np.abs(a.astype(np.float64) - b) <= 64 * 2.0 ** -24 * nrm + 1e-30).all(), t
 
 
 @pytest.mark.parametrize("plant,check", [
