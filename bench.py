@@ -157,14 +157,16 @@ def rand_weight(m27q, torch, dev, t, rc, k, layout=None):
     return m27q.Weight(torch.from_numpy(host).to(dev), t, rb, rc, layout)
 
 
-def timed(torch, fn, ncopies, reps, warm=3):
+def timed(torch, fn, ncopies, reps, warm=3, calls=32):
     """Average us per call of fn(c, stream) over ncopies rotated inputs, captured in a
-    graph; `warm` untimed replays first (the first replays after a stretch of host work
-    run measurably slower: 181 us against 163 for the LM head)."""
-    g = capture(torch, lambda st: [fn(c, st) for c in range(ncopies)])
+    graph of at least `calls` calls (whole rotations), so graph launch boundaries
+    stay rare; `warm` untimed replays first (the first replays after a stretch of
+    host work run measurably slower: 181 us against 163 for the LM head)."""
+    rot = max(1, -(-calls // ncopies))
+    g = capture(torch, lambda st: [fn(c, st) for _ in range(rot) for c in range(ncopies)])
     for _ in range(warm):
         g.replay()
-    return time_graph(torch, g, reps) / ncopies * 1e3
+    return time_graph(torch, g, max(1, reps // rot)) / (rot * ncopies) * 1e3
 
 
 SECTIONS = ("cfg1", "cfg2", "cfg4", "cfg5", "decode")
@@ -248,7 +250,7 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
         m27q.matvec(lm, B.out, logits, stream=st)
         m27q.topk(logits, k, idx, val, scratch, stream=st)
         m27q.sample(idx, val, k, 0.8, 0.05, 0.95, u, tok, stream=st)
-    us = timed(torch, decode_step, 1, max(4, reps // 10))
+    us = timed(torch, decode_step, 1, max(4, reps // 10), calls=1)
     out["decode_step_linears_64_layers"] = {"us": round(us, 1), "tokens_per_s": round(1e6 / us, 1)}
     log(f"decode step of linears: {us:.1f} us")
     return out
@@ -426,15 +428,24 @@ def main():
         return
     B = Buffers(m27q, dev)
 
-    def cold_pass(s):
-        for L in layers:
-            layer_pass(m27q, L, B, s)
+    # A real decode step replays one graph for all its layers, so the layer's
+    # time is measured inside graphs of ROT rotations over the copies (32 layer
+    # passes): a graph launch boundary costs a few microseconds that a layer in
+    # the middle of a decode step does not pay.
+    ROT = 8
+    PG = ROT * copies
+
+    def cold_pass(s, rot=1):
+        for _ in range(rot):
+            for L in layers:
+                layer_pass(m27q, L, B, s)
 
     def warm_pass(s):
-        for _ in range(copies):
+        for _ in range(PG):
             layer_pass(m27q, layers[0], B, s)
 
     log("capturing graphs")
+    g_big = capture(torch, lambda st: cold_pass(st, ROT))
     g_cold = capture(torch, cold_pass)
     g_warm = capture(torch, warm_pass)
     # one graph per copy, for the warm-up and step counts that are not whole rotations
@@ -442,9 +453,12 @@ def main():
 
     def run_steps(n):
         """Exactly n layer passes, continuing the rotation over the copies."""
-        for _ in range(n // copies):
+        q, r = divmod(n, PG)
+        for _ in range(q):
+            g_big.replay()
+        for _ in range(r // copies):
             g_cold.replay()
-        for c in range(n % copies):
+        for c in range(r % copies):
             g_one[c].replay()
 
     run_steps(args.warmup)
@@ -459,21 +473,22 @@ def main():
     e1.synchronize()
     ms_cold = e0.elapsed_time(e1) / args.steps
     reps = max(1, args.steps // copies)
-    ms_warm = time_graph(torch, g_warm, reps) / copies
-    # Spread: 10 batches of whole rotations, each timed by one event pair with
+    greps = max(1, args.steps // PG)
+    ms_warm = time_graph(torch, g_warm, greps) / PG
+    # Spread: 10 batches of the big graph, each timed by one event pair with
     # the batch's replays all enqueued (as the headline is), so the figures
     # are comparable to it.
-    nb = max(1, reps // 10)
-    per = [time_graph(torch, g_cold, nb) / copies * 1e3 for _ in range(10)]
+    nb = max(1, greps // 4)
+    per = [time_graph(torch, g_big, nb) / PG * 1e3 for _ in range(10)]
 
-    # Each product on its own, over the same rotated copies: average launch
-    # duration from HIP events on the replay stream.
+    # Each product on its own, over the same rotated copies (ROT rotations per
+    # graph): average launch duration from HIP events on the replay stream.
     stages = {}
     for name, fn in STAGES.items():
-        g = capture(torch, lambda st, fn=fn: [fn(m27q, L, B, st) for L in layers])
+        g = capture(torch, lambda st, fn=fn: [fn(m27q, L, B, st) for _ in range(ROT) for L in layers])
         for _ in range(3):
             g.replay()
-        ms = time_graph(torch, g, reps) / copies
+        ms = time_graph(torch, g, greps) / PG
         nbytes = stage_bytes(m27q, name)
         stages[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
         log(f"{name}: {ms * 1e3:.2f} us, {stages[name]['GBps']} GB/s")
@@ -510,7 +525,7 @@ def main():
         "config": {"workload": "qwen27b_q4km_decode_layer_linears_m1",
                    "layer": {n: f"{t} {rc}x{k}" for n, t, rc, k in LAYER},
                    "weight_bytes": layer_bytes, "layout": "tiled", "activation": "int8 per-32, fp32 scale",
-                   "cold_copies": copies, "graph": True},
+                   "cold_copies": copies, "graph": True, "layer_passes_per_graph": PG},
         "us_per_layer": round(ms_cold * 1e3, 2),
         "us_per_layer_batches_p10_median_p90": [round(float(np.percentile(per, q)), 2) for q in (10, 50, 90)],
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
