@@ -3,14 +3,16 @@
 
 Workload (Qwen-27B shapes, seeded synthetic weights ~ N(0, 0.02) quantized by
 the oracle's block generators; x ~ N(0, 1)):
-    Q4_K q 6144x5120, k 1024x5120, v 1024x5120  (one launch, shared activation)
-    Q4_K o 5120x6144                            (fused quantization of its output)
-    Q4_K gate, up 17408x5120 + SwiGLU           (one launch, fused output quantization)
-    Q6_K down 5120x17408
-in dependency order.  A step is one such layer pass.  Weights rotate over
-enough distinct device copies (>= 2 x the 256 MB Infinity Cache) that every
-step streams its weights from HBM; a warm (cache-resident) figure is reported
-beside it.  The whole step sequence is captured once in a HIP graph.
+    Q4_K q 6144x5120, k 1024x5120, v 1024x5120  (one launch on the fp32 x)
+    Q4_K o 5120x6144                            (on the q vector, + residual)
+    Q4_K gate, up 17408x5120 + SwiGLU           (one launch, fp32 output)
+    Q6_K down 5120x17408                        (on that fp32 output, + residual)
+in dependency order; every product quantizes its fp32 input inside the
+kernel.  A step is one such layer pass.  Weights rotate over enough distinct
+device copies (>= 2 x the 256 MB Infinity Cache) that every step streams its
+weights from HBM; a warm (cache-resident) figure is reported beside it.  The
+passes replay from HIP graphs of 32 layer passes each, as a decode step
+replays one graph for all its layers.
 
 value = weight bytes of the layer (GGUF, unpadded: 214,671,360 B) / step time.
 """
