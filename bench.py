@@ -392,6 +392,63 @@ def cpu_baseline(ora, host, budget_s=8.0, single_budget_s=3.0):
                       f"itself: the vendored ref/llama.cpp is empty)"}
 
 
+def wave_timeline(m27q, torch, dev, layers, B, trials=3):
+    """Per-wave timeline of each M = 1 product, one launch on cold weights per
+    trial (the last of a run of back-to-back launches), from the measurement build (libm27q_timeline.so: the same kernels
+    recording, per wave, the real-time counter at start, once the activation is
+    staged in LDS, and at the end, with the wave's CU).  Prints one summary per
+    launch: quantiles (p0/p10/p50/p90/p100, microseconds) of wave start,
+    staging time, compute time and end; the mean time CUs sit idle between
+    their last wave's end and the launch's end; and the CUs' end times grouped
+    by how many workgroups each CU ran."""
+    import collections
+    import ctypes as C
+    L = m27q.lib()
+    L.m27q_timeline_read.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    y = torch.empty(17408, dtype=torch.float32, device=dev)
+    prods = dict(STAGES)
+    prods["cfg1"] = lambda m27q, Lw, B, s: m27q.matvec(Lw["gate"], B.x, y, stream=s)
+    N = 1 << 16
+    q = lambda a: "/".join(f"{np.percentile(a, p):.2f}" for p in (0, 10, 50, 90, 100))
+    for name, fn in prods.items():
+        for trial in range(trials):
+            if L.m27q_timeline_clear() != 0:
+                raise RuntimeError("m27q_timeline_clear failed")
+            # The recorded launch follows other launches with nothing in
+            # between, as in a decode step: a launch that follows a host copy
+            # or an idle queue starts its waves on the 8 XCDs up to ~4 us
+            # apart, one that follows a kernel within ~0.2 us.  Every launch
+            # writes the same slots, so the records are the last launch's.
+            for r in range(2 * len(layers) + trial + 1):
+                fn(m27q, layers[r % len(layers)], B, None)
+            torch.cuda.synchronize()
+            t = np.zeros((N, 3), np.uint64)
+            hw = np.zeros((N, 3), np.uint32)
+            if L.m27q_timeline_read(t.ctypes.data, hw.ctypes.data, N) != 0:
+                raise RuntimeError("m27q_timeline_read failed")
+            used = t[:, 0] > 0
+            ts, h = t[used].astype(np.int64), hw[used]
+            st, sg, en = [(ts[:, j] - ts[:, 0].min()) / 100.0 for j in range(3)]  # 100 MHz counter
+            hid = h[:, 0].astype(np.int64)
+            cu = ((h[:, 1].astype(np.int64) & 0xf) << 8) | (((hid >> 13) & 7) << 5) | (((hid >> 12) & 1) << 4) | ((hid >> 8) & 0xf)
+            blk = h[:, 2] >> 8
+            cu_blocks, cu_end = collections.defaultdict(set), collections.defaultdict(float)
+            for c, b, e in zip(cu.tolist(), blk.tolist(), en.tolist()):
+                cu_blocks[c].add(b)
+                cu_end[c] = max(cu_end[c], e)
+            span = float(en.max())
+            by = collections.defaultdict(list)
+            for c, b in cu_blocks.items():
+                by[len(b)].append(cu_end[c])
+            idle = float(np.mean([span - e for e in cu_end.values()]))
+            print(f"{name:8s} launch {trial}: waves {len(ts)} on {len(cu_blocks)} CUs, span {span:.2f} us | "
+                  f"start {q(st)} | staging {q(sg - st)} | compute {q(en - sg)} | end {q(en)} | "
+                  f"mean CU idle at the end {idle:.2f} us ({100 * idle / span:.0f}%)", flush=True)
+            print("    CU end by workgroups per CU {n: (CUs, mean us, max us)}:",
+                  {k: (len(v), round(float(np.mean(v)), 2), round(float(np.max(v)), 2)) for k, v in sorted(by.items())},
+                  flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,6 +460,9 @@ def main():
     ap.add_argument("--only", default="",
                     help="comma-separated suite sections (cfg1,cfg2,cfg4,cfg5,decode) to run alone, without the "
                          "layer timing; prints their figures (for profiler runs), not the benchmark line")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-wave timeline of each M = 1 product from the measurement build "
+                         "(libm27q_timeline.so); prints summaries, not the benchmark line")
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain 512 MiB device copy (the reference point that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -415,6 +475,8 @@ def main():
     import torch
     import oracle as ora
     m27q = load_pkg()
+    if args.timeline:
+        m27q.LIB_PATH = os.path.join(os.path.dirname(m27q.LIB_PATH), "libm27q_timeline.so")
     dev = torch.device("cuda:0")
     layer_bytes = sum(m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256 for _, t, rc, k in LAYER)
     copies = args.copies or max(2, -(-2 * MALL_BYTES // layer_bytes) + 1)
@@ -429,6 +491,9 @@ def main():
         print(json.dumps({"only": secs, "suite": suite(m27q, torch, dev, layers, max(1, args.steps // copies), secs)}))
         return
     B = Buffers(m27q, dev)
+    if args.timeline:
+        wave_timeline(m27q, torch, dev, layers, B)
+        return
 
     # A real decode step replays one graph for all its layers, so the layer's
     # time is measured inside graphs of ROT rotations over the copies (32 layer

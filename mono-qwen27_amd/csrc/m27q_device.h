@@ -173,9 +173,15 @@ __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
 
 // Eight consecutive values per lane, one group per 4 consecutive lanes
 // (lanes 4a .. 4a+3; lane l of the group holds values 8 l .. 8 l + 7).
-// Returns the 8 codes packed as bytes; *d_out and *s_out as in quant32.
-// Bit-identical to quant32 on the same group: the max, the divides, the
-// multiplies and the integer sums see the same values.
+// Returns the 8 codes packed as bytes; *d_out as in quant32 (every lane), and
+// *s_out as in quant32 in the group's first lane 4a only.  Bit-identical to
+// quant32 on the same group: the max, the divides, the multiplies and the
+// integer sums see the same values.  The staging of every fp32-input product
+// runs this once per 8 values, so it is kept short: the code sums are two dot
+// products with ones, and only the lane that stores them packs them (a
+// per-lane choice of the packing order compiled to a branch).  Measured: the
+// layer 0.6 us faster; dropping the clamp too (it never acts) made the
+// compiler's schedule of config 1's loop 0.4 us slower.
 __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uint32_t *s_out) {
     float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                        fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
@@ -183,14 +189,13 @@ __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uin
     amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
     const float d = div127(amax);
     const float id = inv_scale(d);
-    const int q0 = quant_code(a.x, id), q1 = quant_code(a.y, id), q2 = quant_code(a.z, id), q3 = quant_code(a.w, id);
-    const int q4 = quant_code(b.x, id), q5 = quant_code(b.y, id), q6 = quant_code(b.z, id), q7 = quant_code(b.w, id);
-    int s = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
-    s += dpp_i<kDppXor1>(s);  // lanes 0-1: values 0..15; lanes 2-3: values 16..31
-    const int s_other = dpp_i<kDppXor2>(s);
+    const uint32_t lo = pack_codes(quant_code(a.x, id), quant_code(a.y, id), quant_code(a.z, id), quant_code(a.w, id));
+    const uint32_t hi = pack_codes(quant_code(b.x, id), quant_code(b.y, id), quant_code(b.z, id), quant_code(b.w, id));
+    int s = dot4((int)hi, 0x01010101, dot4((int)lo, 0x01010101, 0));
+    s += dpp_i<kDppXor1>(s);  // lanes 4a, 4a+1: values 0..15; lanes 4a+2, 4a+3: values 16..31
     *d_out = d;
-    *s_out = (threadIdx.x & 2) == 0 ? pack_sums(s, s_other) : pack_sums(s_other, s);
-    return make_uint2(pack_codes(q0, q1, q2, q3), pack_codes(q4, q5, q6, q7));
+    *s_out = pack_sums(s, dpp_i<kDppXor2>(s));
+    return make_uint2(lo, hi);
 }
 
 // IQ4_NL / IQ4_XS table (exec:51-55) as bytes: entries 0..3, 4..7, 8..11, 12..15.

@@ -163,9 +163,34 @@ __device__ __forceinline__ void quant_output(const GemvParams &p, int row0, int 
     }
 }
 
+#ifdef M27Q_WAVE_TIMELINE
+// Measurement build only (libm27q_timeline.so): per wave of the last launch,
+// {start, activation staged, end} from the 100 MHz real-time counter and
+// {HW_ID, XCC_ID, workgroup << 8 | wave}.  Slots past the capacity are dropped.
+constexpr int kTimelineCap = 1 << 16;
+__device__ unsigned long long g_timeline_t[kTimelineCap][3];
+__device__ unsigned int g_timeline_hw[kTimelineCap][3];
+
+__device__ __forceinline__ void timeline_record(unsigned long long t0, unsigned long long t1, int nw, int wave) {
+    const unsigned long long t2 = __builtin_amdgcn_s_memrealtime();
+    const int slot = (int)blockIdx.x * nw + wave;
+    if ((threadIdx.x & 63) == 0 && slot < kTimelineCap) {
+        g_timeline_t[slot][0] = t0;
+        g_timeline_t[slot][1] = t1;
+        g_timeline_t[slot][2] = t2;
+        g_timeline_hw[slot][0] = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID
+        g_timeline_hw[slot][1] = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // XCC_ID
+        g_timeline_hw[slot][2] = (blockIdx.x << 8) | (unsigned)wave;
+    }
+}
+#endif
+
 template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>
 __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
+#ifdef M27Q_WAVE_TIMELINE
+    const unsigned long long tl_start = __builtin_amdgcn_s_memrealtime();
+#endif
     constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int NR = TPW * kTileRows;  // rows per workgroup
@@ -219,6 +244,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     const ActLds act{(const int8_t *)smem, (const float *)(smem + Kp), (const uint32_t *)(smem + Kp + Kp / 8)};
     float *red = (float *)(smem + Kp + Kp / 4);  // [NM][KS][NR]
     __syncthreads();
+#ifdef M27Q_WAVE_TIMELINE
+    const unsigned long long tl_staged = __builtin_amdgcn_s_memrealtime();
+#endif
 
     float acc[NM][WT];
 #pragma unroll
@@ -283,6 +311,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     }
     if constexpr (NR % 32 == 0)
         if (p.oq) quant_output<NR>(p, tile0 * kTileRows, rc, v);
+#ifdef M27Q_WAVE_TIMELINE
+    timeline_record(tl_start, tl_staged, C::NW, wave);
+#endif
 }
 
 // ------------------------------------------------ fp32-activation products --
@@ -536,3 +567,20 @@ hipError_t launch_gemv_f32(uint32_t type, int layout, const GemvParams &p, int g
 }
 
 }  // namespace m27q
+
+#ifdef M27Q_WAVE_TIMELINE
+// Copies the first n records to the host (n <= 65536); clears them.
+extern "C" __attribute__((visibility("default"))) int m27q_timeline_read(unsigned long long *t, unsigned int *hw, int n) {
+    if (n < 0 || n > m27q::kTimelineCap) return -1;
+    if (hipMemcpyFromSymbol(t, HIP_SYMBOL(m27q::g_timeline_t), (size_t)n * 24, 0, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpyFromSymbol(hw, HIP_SYMBOL(m27q::g_timeline_hw), (size_t)n * 12, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return -2;
+    return 0;
+}
+extern "C" __attribute__((visibility("default"))) int m27q_timeline_clear() {
+    static unsigned long long zero[m27q::kTimelineCap][3];
+    return hipMemcpyToSymbol(HIP_SYMBOL(m27q::g_timeline_t), zero, sizeof zero, 0, hipMemcpyHostToDevice) == hipSuccess
+               ? 0
+               : -1;
+}
+#endif
