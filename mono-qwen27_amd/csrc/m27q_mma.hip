@@ -711,7 +711,9 @@ static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
 // Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 16: a
 // launch of fewer than 320 row sets (q/k/v, o and down with two-set tiles)
 // splits K over 8 waves, a larger one over 4; more waves per set cost more
-// than they hide.  Two row sets per tile whenever at most 8 tokens are left
+// than they hide.  One-set tiles (M > 8) on K <= 6144 (q/k/v, gate/up, o)
+// also split over 8: at M = 16 gate/up 35.6 us against 37.7, q/k/v and o
+// 0.3 us faster; down (K = 17408) was 1.6 us slower so.  Two row sets per tile whenever at most 8 tokens are left
 // and the product has at least 128 sets of 32 rows (every product of the
 // layer): down at M = 8 takes 21.7 us against 28.8 with one-set tiles.
 #ifndef M27Q_MM_KS
@@ -724,7 +726,7 @@ template <class T, int PK>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
     long long sets = 0;
     for (int i = 0; i < p.nmat; ++i) sets += (p.rc[i] + 16 * PK - 1) / (16 * PK);
-    const int ks = M27Q_MM_KS ? M27Q_MM_KS : sets < 320 ? 8 : 4;
+    const int ks = M27Q_MM_KS ? M27Q_MM_KS : (sets < 320 || (PK == 1 && p.K <= 6144)) ? 8 : 4;
     switch (ks) {
         case 2: return launch_mfma_t<T, PK, 2>(p, m0, s);
         case 8: return launch_mfma_t<T, PK, 8>(p, m0, s);
