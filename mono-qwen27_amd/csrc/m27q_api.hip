@@ -44,17 +44,21 @@ int device_attr(hipDeviceAttribute_t a, std::atomic<int> (&cache)[kMaxDevices], 
     return v;
 }
 
+}  // namespace
+
 // Compute units of the current device (256 on MI355X), for balanced tiling.
-int cu_count() {
+int m27q::cu_count() {
     static std::atomic<int> cache[kMaxDevices];
     return device_attr(hipDeviceAttributeMultiprocessorCount, cache, 256);
 }
 
 // LDS limit of one workgroup on the current device (160 KiB on gfx950).
-size_t lds_limit() {
+size_t m27q::lds_limit() {
     static std::atomic<int> cache[kMaxDevices];
     return (size_t)device_attr(hipDeviceAttributeMaxSharedMemoryPerBlock, cache, 64 * 1024);
 }
+
+namespace {
 
 int k_of(const m27q_weight *w) { return (int)w->row_blocks * block_elems(w->ggml_type); }
 

@@ -111,6 +111,9 @@ hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream
 // int8-MFMA small-M products (m27q_mma.hip): TILED weights, any M (16 tokens
 // per launch).
 size_t matmul_mfma_lds_bytes(uint32_t type);
+// The current device's CU count and LDS bytes per workgroup (cached per device).
+int cu_count();
+size_t lds_limit();
 hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
 
 }  // namespace m27q

@@ -690,6 +690,234 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     }
 }
 
+// ------------------------------------------- resident activation rows --
+// One-set tiles (16 tokens) over many row sets.  The kernel above re-stages
+// every unit's 16 activation rows in each wave (4.4 KB per unit against
+// 2.3 KB of Q4_K weights for 16 rows); here each workgroup stages the M x K
+// activation codes and scales into LDS once and then streams its share of the
+// row sets' weights through per-wave staging areas as above.
+//
+// LDS: TK token records of Kp + 16 bytes (Kp = the units' K; the 16-byte pad
+// keeps the token stride at 16 mod 128 bytes, as the per-unit records'), a
+// zero record (Q6_K's zero-split views), dT [Kp/32][TK] and, for Q4_K / Q5_K,
+// aT [Kp/32][TK] floats, then one area per wave (the unit's weight records and
+// side area, later its two partial sums).
+//
+// Work: workgroup g of G takes row sets [S g / G, S (g + 1) / G) of the S sets
+// of all matrices; its units (set, k unit) in order are split into NWV
+// contiguous runs, one per wave.  The host keeps the sets per workgroup at
+// most NWV, so a run has at most upr units and covers at most two sets: the
+// wave keeps the first set's sums in registers while it accumulates the
+// second.  At the end each set's sums are added over the waves that covered
+// it, in wave order.
+template <class T>
+struct XStage {
+    using SG = Stage<T, 1>;
+    static constexpr int G = T::kGroups, TK = 16, UE = SG::UE, UB = SG::UB;
+    static constexpr int kWaveBytes = (SG::kW + 16 + 15) / 16 * 16;  // weights, side area, dummy slot
+    static constexpr int oDummy = SG::kW;
+    static_assert(kWaveBytes >= 2 * 4 * kWave * 4, "two partial-sum slots per wave area");
+    static constexpr int xrow(int upr) { return upr * UE + 16; }
+    static constexpr int oZero(int upr) { return TK * xrow(upr); }
+    static constexpr int oDT(int upr) { return oZero(upr) + UE; }
+    static constexpr int oAT(int upr) { return oDT(upr) + upr * G * TK * 4; }
+    static constexpr int oWaves(int upr) { return (oAT(upr) + (T::kAux ? upr * G * TK * 4 : 0) + 15) / 16 * 16; }
+    static constexpr size_t bytes(int upr, int nwv) { return (size_t)oWaves(upr) + (size_t)nwv * kWaveBytes; }
+};
+
+// 16-byte activation chunks each thread has in flight while staging: 16
+// tokens x 6144 codes / 1024 threads in one round.
+#ifndef M27Q_XRES_BATCH
+#define M27Q_XRES_BATCH 6
+#endif
+constexpr int kXBatch = M27Q_XRES_BATCH;
+template <class T, int NWV>
+__global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiParams p, int m0) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    using XS = XStage<T>;
+    using SG = typename XS::SG;
+    constexpr int G = T::kGroups, NS = T::kSteps, TK = 16, UE = SG::UE, UB = SG::UB;
+    constexpr int CPU = UB / 16;
+    constexpr int NP = T::template kPieces<1>;
+    const int lane = (int)(threadIdx.x & 63);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nth = NWV * kWave;
+    const Lane<1> L(lane);
+    const int upr = p.upr, K = p.K, Kp = upr * UE, ngk = K / 32;
+    const int xrow = XS::xrow(upr);
+    const int Mloc = min(p.M - m0, TK);
+    uint8_t *X = smem;
+    float *dT = (float *)(smem + XS::oDT(upr)), *aT = (float *)(smem + XS::oAT(upr));
+    uint8_t *wl = smem + XS::oWaves(upr) + wave * XS::kWaveBytes;
+
+    // 1. The activation rows, codes and scales, into LDS.  Padding tokens
+    // (past M) read token m0's codes and get zero scales; codes past K (a
+    // Q8_0 unit's padding) are zero.
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(p.xq, (uint32_t)p.M * (uint32_t)K);
+    {
+        const int cpr = Kp / 16, nch = TK * cpr;
+        for (int i0 = (int)threadIdx.x; i0 < nch; i0 += kXBatch * nth) {
+            v4u v[kXBatch];
+#pragma unroll
+            for (int b = 0; b < kXBatch; ++b) {
+                const int i = i0 + b * nth, tok = i / cpr, j = i % cpr;
+                const int src = m0 + (tok < Mloc ? tok : 0);
+                v[b] = (i < nch && 16 * j < K) ? buf_ld16(xr, (uint32_t)src * (uint32_t)K + 16u * (uint32_t)j, 0u)
+                                               : v4u{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int b = 0; b < kXBatch; ++b) {
+                const int i = i0 + b * nth;
+                if (i < nch) *(v4u *)(X + (i / cpr) * xrow + 16 * (i % cpr)) = v[b];
+            }
+        }
+        if ((int)threadIdx.x < UE / 16) *(v4u *)(smem + XS::oZero(upr) + 16 * threadIdx.x) = v4u{0u, 0u, 0u, 0u};
+        const int ns = upr * G * TK;
+        for (int i = (int)threadIdx.x; i < ns; i += nth) {
+            const int g = i / TK, tok = i % TK;
+            const bool in = tok < Mloc && g < ngk;
+            const size_t o = (size_t)(m0 + (in ? tok : 0)) * ngk + (in ? g : 0);
+            const float d = in ? p.xd[o] : 0.f;
+            dT[i] = d;
+            if constexpr (T::kAux) aT[i] = in ? T::stage_aux(d, p.xs[o]) : 0.f;
+        }
+    }
+
+    // 2. This workgroup's sets and this wave's run of units.
+    const int S = p.wg_start[p.nmat];
+    const int s0 = (int)((long long)S * blockIdx.x / gridDim.x);
+    const int nsets = (int)((long long)S * (blockIdx.x + 1) / gridDim.x) - s0;
+    const int N = nsets * upr;
+    const int ua = (int)((long long)N * wave / NWV), ub = (int)((long long)N * (wave + 1) / NWV);
+
+    // Weight staging map of this lane (the same for every set; tiles past the
+    // matrix's end reread its last tile).
+    int wdst[SG::kNW], wt[SG::kNW], wc[SG::kNW];
+#pragma unroll
+    for (int n = 0; n < SG::kNW; ++n) {
+        const int id = n * kWave + lane;
+        const bool ok = id < SG::kWChunks;
+        wt[n] = ok ? id / CPU : 0;
+        wc[n] = ok ? id % CPU : 0;
+        wdst[n] = ok ? T::lds_dst(wt[n], wc[n], SG::kSide) : XS::oDummy;
+    }
+    v4u rw[SG::kNW];
+    auto issue = [&](int idx) __attribute__((always_inline)) {
+        const int gs = s0 + idx / upr, u = idx % upr;
+        int mi = 0;
+#pragma unroll
+        for (int k = 1; k < kMaxMulti; ++k)
+            if (k < p.nmat && gs >= p.wg_start[k]) mi = k;
+        const int rc = p.rc[mi], ntiles8 = (rc + kTileRows - 1) / kTileRows;
+        const int tile0 = (gs - p.wg_start[mi]) * 2;
+        const __amdgpu_buffer_rsrc_t wr = buf_rsrc(p.W[mi], (uint32_t)ntiles8 * (uint32_t)(upr * UB));
+#pragma unroll
+        for (int n = 0; n < SG::kNW; ++n) {
+            const int tile = min(tile0 + wt[n], ntiles8 - 1);
+            rw[n] = buf_ld16(wr, (uint32_t)tile * (uint32_t)(upr * UB) + 16u * (uint32_t)wc[n], (uint32_t)u * UB);
+        }
+    };
+    auto commit = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+    };
+
+    const int wrow = L.c;  // the lane's weight row within the set
+    const int atok = L.c;  // and its token
+    const uint8_t *xa = X + atok * xrow + 8 * L.r;
+    const uint8_t *xz = smem + XS::oZero(upr) + 8 * L.r;
+    const ScaleLds<1> sl{dT, aT};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, u4[4] = {0.f, 0.f, 0.f, 0.f}, first[4] = {0.f, 0.f, 0.f, 0.f};
+    v4f cm = v4f{0.f, 0.f, 0.f, 0.f};  // Q4_K min term
+    auto compute = [&](int idx) __attribute__((always_inline)) {
+        const int u = idx % upr;
+        const uint8_t *ab[NP];
+        if constexpr (NP == 1) {
+            ab[0] = xa + u * UE;
+        } else {  // Q6_K: quarters 0-1 (sub-block 0) and 2-3 (sub-block 1)
+            ab[0] = L.q < 2 ? xa + u * UE : xz;
+            ab[1] = L.q < 2 ? xz : xa + u * UE;
+        }
+        typename T::template Frag<1> f0, f1;
+        AFrag<NP> x0, x1;
+        T::template load<1>(f0, wl, wrow, L.r, 0, SG::kSide);
+        load_act<NP>(x0, ab, 0);
+        if constexpr (NS == 2) {
+            T::template load<1>(f1, wl, wrow, L.r, 1, SG::kSide);
+            load_act<NP>(x1, ab, 1);
+        }
+        compute_half<T, 1, 0>(f0, x0, sl, u * G, L, true, atok, acc, u4, cm);
+        if constexpr (NS == 2) compute_half<T, 1, 1>(f1, x1, sl, u * G, L, true, atok, acc, u4, cm);
+    };
+    // The first set's sums move to `first` when the run enters the second.
+    auto close_first = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            first[e] = T::kAux ? acc[e] - cm[e] : acc[e];
+            acc[e] = 0.f;
+        }
+        cm = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    // The first unit's weights load while the activation staging completes.
+    if (ua < ub) issue(ua);
+    __syncthreads();
+
+    // 3. The run, one unit ahead as in the kernel above (unconditional loads,
+    // last unit peeled).  Waves with an empty run skip it.
+    const int n_first = ua < ub ? min(ub, (ua / upr + 1) * upr) - ua : 0;  // units of the first set
+    if (ua < ub) {
+        commit();
+        for (int k = 0; k + 1 < ub - ua; ++k) {
+            issue(ua + k + 1);
+            compute(ua + k);
+            if (k + 1 == n_first) close_first();
+            commit();
+        }
+        compute(ub - 1);
+        if (ub - ua == n_first) {
+            close_first();
+        } else if (T::kAux) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] -= cm[e];
+        }
+    }
+
+    // 4. Partial sums -> this wave's area (slot 0: first set, slot 1: second),
+    // then each output adds the waves that covered its set, in wave order.
+    {
+        float *P = (float *)wl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            P[e * kWave + lane] = first[e];
+            P[4 * kWave + e * kWave + lane] = acc[e];
+        }
+    }
+    __syncthreads();
+    for (int idx = (int)threadIdx.x; idx < nsets * 4 * kWave; idx += nth) {
+        const int sl_ = idx / (4 * kWave), r = idx % (4 * kWave), e = r / kWave, ln = r % kWave;
+        const int lo = sl_ * upr, hi = lo + upr;  // the set's units in the workgroup's order
+        float v = 0.f;
+        for (int w = 0; w < NWV; ++w) {
+            const int a = (int)((long long)N * w / NWV), b = (int)((long long)N * (w + 1) / NWV);
+            if (a < hi && b > lo) {
+                const int slot = a / upr == sl_ ? 0 : 1;
+                v += ((const float *)(smem + XS::oWaves(upr) + w * XS::kWaveBytes))[slot * 4 * kWave + r];
+            }
+        }
+        const int gs = s0 + sl_;
+        int mi = 0;
+#pragma unroll
+        for (int k = 1; k < kMaxMulti; ++k)
+            if (k < p.nmat && gs >= p.wg_start[k]) mi = k;
+        const Lane<1> O(ln);
+        const int rc = p.rc[mi], row = (gs - p.wg_start[mi]) * 16 + O.c, tok = 4 * O.r + e;
+        if (row < rc && tok < Mloc) {
+            const size_t o = (size_t)(m0 + tok) * rc + row;
+            p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
+        }
+    }
+}
+
 template <class T, int PK, int KS>
 static size_t mfma_lds() {
     return (size_t)KS * Stage<T, PK>::kBytes;
@@ -706,6 +934,41 @@ static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
     p.wg_start[p.nmat] = total;
     hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
     return hipGetLastError();
+}
+
+// The resident-activation kernel serves a launch of 16 tokens when every CU
+// gets at least M27Q_XRES_MIN_SETS_PER_CU row sets (the activation staging is
+// paid once per workgroup) and its LDS fits.  16 waves per workgroup (every
+// type compiles within 128 registers, 4 waves per SIMD).  Measured on the
+// layer's gate/up (2176 sets): 32 us against 36 at M = 16, 32.5 against 33.5
+// at M = 12, where the layer's other launches ran about 0.3 us slower each
+// after it, so only full 16-token launches take it; q/k/v (2 sets per CU)
+// took 14 us against 9.5 with it.
+#ifndef M27Q_XRES_MIN_SETS_PER_CU
+#define M27Q_XRES_MIN_SETS_PER_CU 4
+#endif
+template <class T>
+constexpr int xres_waves() {
+    return 16;
+}
+template <class T>
+static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *err) {
+    constexpr int NWV = xres_waves<T>();
+    int S = 0;
+    for (int i = 0; i < p.nmat; ++i) {
+        p.wg_start[i] = S;
+        S += (p.rc[i] + 15) / 16;
+    }
+    p.wg_start[p.nmat] = S;
+    const int cus = cu_count();
+    if (p.M - m0 < 16 || S < M27Q_XRES_MIN_SETS_PER_CU * cus) return false;
+    const size_t lds = XStage<T>::bytes(p.upr, NWV);
+    if (lds > lds_limit()) return false;
+    // at most NWV sets per workgroup, so each wave's run covers at most two
+    const int G = std::min(S, std::max(cus, (S + NWV - 1) / NWV));
+    hipLaunchKernelGGL((k_matmul_mfma_xres<T, NWV>), dim3(G), dim3(kWave * NWV), lds, s, p, m0);
+    *err = hipGetLastError();
+    return true;
 }
 
 // Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 16: a
@@ -741,7 +1004,11 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
     for (int m0 = 0; m0 < p.M;) {
         const int left = p.M - m0;
         const bool pk2 = left <= 8 && sets32 >= M27Q_MM_PK2_MIN_SETS;
-        const hipError_t e = pk2 ? launch_mfma_pk<T, 2>(p, m0, s) : launch_mfma_pk<T, 1>(p, m0, s);
+        hipError_t e = hipSuccess;
+        if (pk2)
+            e = launch_mfma_pk<T, 2>(p, m0, s);
+        else if (!launch_xres<T>(p, m0, s, &e))
+            e = launch_mfma_pk<T, 1>(p, m0, s);
         if (e != hipSuccess) return e;
         m0 += pk2 ? Pack<2>::TK : Pack<1>::TK;
     }

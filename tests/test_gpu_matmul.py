@@ -36,6 +36,12 @@ CASES = [  # type, rows, K, M, layout
     # tiles), and both ends of the range with a ragged last tile (513 and 768
     # tiles)
     ("Q4_K", 5120, 6144, 2, 1), ("Q6_K", 4100, 2048, 2, 1), ("Q4_K", 6141, 2048, 2, 1),
+    # resident activation rows (16-token launches with >= 4 row sets per CU:
+    # 1025 sets of 16 rows on 256 CUs), every type, a partial last set, a
+    # partial Q8_0 unit (K = 1056), and 16 + 9 tokens (the resident launch,
+    # then the per-unit staging one)
+    ("Q4_K", 16390, 1024, 16, 1), ("Q6_K", 16390, 1024, 16, 1), ("Q8_0", 16390, 1056, 16, 1),
+    ("Q5_K", 16390, 1024, 25, 1), ("IQ4_XS", 16390, 1024, 32, 1),
 ]
 
 
@@ -83,4 +89,27 @@ def test_matmul_multi_vs_oracle(m27q, ora, dev, M):
         got = to_host(Y).astype(np.float64)
         for m in sorted({0, M // 2, M - 1}):
             want, nrm = ora.gemv_act(m27q.Q4_K, wb, 20, rc, q[m], d[m], s[m])
+            assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)
+
+
+@pytest.mark.parametrize("M", [16, 32])
+def test_matmul_multi_resident_vs_oracle(m27q, ora, dev, M):
+    """Two weights of one K in one resident-activation launch (513 + 513 row
+    sets, the second matrix's sets following the first's in the workgroups'
+    runs), each against the integer-dot oracle."""
+    import torch
+    k, shapes = 1024, [8200, 8200]
+    wbs = [ora.synth_weights(m27q.Q4_K, rc, k, seed=70 + i) for i, rc in enumerate(shapes)]
+    ws = [m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 4, rc, m27q.TILED, dev) for wb, rc in zip(wbs, shapes)]
+    X = np.random.default_rng(M + 9).standard_normal((M, k)).astype(np.float32)
+    act = m27q.Act(M, k, dev)
+    m27q.quant_act(to_dev(X, dev), act)
+    Ys = [torch.empty((M, rc), dtype=torch.float32, device=dev) for rc in shapes]
+    say("matmul multi resident", M)
+    m27q.matmul_q8_multi(ws, act, Ys)
+    q, d, s = act_host(m27q, act)
+    for wb, rc, Y in zip(wbs, shapes, Ys):
+        got = to_host(Y).astype(np.float64)
+        for m in sorted({0, M // 2, M - 1}):
+            want, nrm = ora.gemv_act(m27q.Q4_K, wb, 4, rc, q[m], d[m], s[m])
             assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)
