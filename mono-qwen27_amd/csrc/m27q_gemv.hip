@@ -448,7 +448,10 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfgQ: return launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s);
         case kCfg81: return launch_q8_cfg<T, LAYOUT, Cfg81, SWIGLU, XF32>(p, s);
         case kCfg42: return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
-        case kCfg84: return launch_q8_cfg<T, LAYOUT, Cfg84, SWIGLU, XF32>(p, s);
+        case kCfg84:  // products without the SwiGLU epilogue only (with it, four
+                      // tiles per wave of two matrices spill registers)
+            if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg84, SWIGLU, XF32>(p, s);
+            return hipErrorInvalidValue;
         case kCfg161:  // chosen for small products without the SwiGLU epilogue only
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg161, SWIGLU, XF32>(p, s);
             return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
