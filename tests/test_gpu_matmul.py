@@ -42,6 +42,10 @@ CASES = [  # type, rows, K, M, layout
     # then the per-unit staging one)
     ("Q4_K", 16390, 1024, 16, 1), ("Q6_K", 16390, 1024, 16, 1), ("Q8_0", 16390, 1056, 16, 1),
     ("Q5_K", 16390, 1024, 25, 1), ("IQ4_XS", 16390, 1024, 32, 1),
+    # two row sets per tile over 1025 sets of 32 rows (a last set of 8 rows),
+    # every type, padding tokens
+    ("Q4_K", 32776, 512, 8, 1), ("Q6_K", 32776, 768, 5, 1), ("Q8_0", 32776, 160, 7, 1),
+    ("Q5_K", 32776, 512, 3, 1), ("IQ4_XS", 32776, 512, 8, 1),
 ]
 
 
@@ -92,13 +96,14 @@ def test_matmul_multi_vs_oracle(m27q, ora, dev, M):
             assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)
 
 
-@pytest.mark.parametrize("M", [16, 32])
-def test_matmul_multi_resident_vs_oracle(m27q, ora, dev, M):
-    """Two weights of one K in one resident-activation launch (513 + 513 row
-    sets, the second matrix's sets following the first's in the workgroups'
-    runs), each against the integer-dot oracle."""
+@pytest.mark.parametrize("M,rows", [(16, 8200), (32, 8200), (7, 16400)])
+def test_matmul_multi_resident_vs_oracle(m27q, ora, dev, M, rows):
+    """Two weights of one K in one launch over 1026 row sets: at M = 16 and 32
+    the resident-activation kernel (the second matrix's sets following the
+    first's in the workgroups' runs), at M = 7 the two-set per-unit kernel;
+    each against the integer-dot oracle."""
     import torch
-    k, shapes = 1024, [8200, 8200]
+    k, shapes = 1024, [rows, rows]
     wbs = [ora.synth_weights(m27q.Q4_K, rc, k, seed=70 + i) for i, rc in enumerate(shapes)]
     ws = [m27q.Weight.upload(wb.reshape(-1), m27q.Q4_K, 4, rc, m27q.TILED, dev) for wb, rc in zip(wbs, shapes)]
     X = np.random.default_rng(M + 9).standard_normal((M, k)).astype(np.float32)
