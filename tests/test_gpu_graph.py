@@ -4,7 +4,8 @@ equal the same calls run eagerly on the same inputs, bit for bit.
 The library allocates, clears and synchronizes nothing (the top-k counter is
 reset by a kernel), so the whole step -- embedding gather, q/k/v, o with
 residual, gate/up with the fused output quantization, down, the small-M
-products, the LM head, top-k and sampling -- can be captured, as the
+products (the resident-activation kernel included), the LM head, top-k and
+sampling -- can be captured, as the
 reference captures its step (exec:2353-2360).  Between replays the inputs are
 rewritten by eager copies and the outputs read back, with synchronizations in
 between, so stale state carried from one replay to the next would show."""
@@ -27,7 +28,8 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     for name, t, rc, k, seed in (("emb", m27q.Q6_K, 4096, 5120, 1), ("q", m27q.Q4_K, 1024, 5120, 2),
                                  ("o", m27q.Q4_K, 5120, 1024, 3), ("gate", m27q.Q4_K, 2048, 5120, 4),
                                  ("up", m27q.Q4_K, 2048, 5120, 5), ("down", m27q.Q6_K, 5120, 2048, 6),
-                                 ("lm", m27q.Q6_K, 8192, 5120, 7)):
+                                 ("lm", m27q.Q6_K, 8192, 5120, 7),
+                                 ("big", m27q.Q4_K, 16400, 5120, 8)):  # resident activation rows at M = 16
         W[name] = m27q.Weight.upload(ora.synth_weights(t, rc, k, seed=seed).reshape(-1), t,
                                      k // m27q.BLOCK_ELEMS[t], rc, m27q.TILED, dev)
     k = 40
@@ -46,6 +48,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     act16 = m27q.Act(16, 5120, dev)
     X16 = torch.empty((16, 5120), dtype=torch.float32, device=dev)
     Y16 = torch.empty((16, 2048), dtype=torch.float32, device=dev)
+    Y16b = torch.empty((16, 16400), dtype=torch.float32, device=dev)
     act5 = m27q.Act(5, 5120, dev)
     X5 = torch.empty((5, 5120), dtype=torch.float32, device=dev)
     Y5 = torch.empty((5, 8192), dtype=torch.float32, device=dev)      # two row sets per tile
@@ -56,7 +59,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
     idx = torch.empty(k, dtype=torch.int32, device=dev)
     val = torch.empty(k, dtype=torch.float32, device=dev)
     tok = torch.empty(1, dtype=torch.int32, device=dev)
-    outs = [x, qv, h, f, fq.buf, out, out2, Y2, Y16, Y5, Y5q, Y5g, logits, idx, val, tok]
+    outs = [x, qv, h, f, fq.buf, out, out2, Y2, Y16, Y16b, Y5, Y5q, Y5g, logits, idx, val, tok]
 
     def step(s):
         m27q.embed_rows(W["emb"], ids, x, bad, stream=s)
@@ -69,6 +72,7 @@ def test_decode_step_graph_replays_match_eager(m27q, ora, dev):
         m27q.matmul_q8(W["q"], act2, Y2, stream=s)
         m27q.quant_act(X16, act16, stream=s)
         m27q.matmul_q8(W["gate"], act16, Y16, stream=s)
+        m27q.matmul_q8(W["big"], act16, Y16b, stream=s)
         m27q.quant_act(X5, act5, stream=s)
         m27q.matmul_q8(W["lm"], act5, Y5, stream=s)
         m27q.matmul_q8_multi([W["q"], W["gate"]], act5, [Y5q, Y5g], stream=s)
