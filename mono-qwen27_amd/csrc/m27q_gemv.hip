@@ -448,8 +448,9 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfgQ: return launch_q8_cfg<T, LAYOUT, CfgQ, SWIGLU, XF32>(p, s);
         case kCfg81: return launch_q8_cfg<T, LAYOUT, Cfg81, SWIGLU, XF32>(p, s);
         case kCfg42: return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
-        case kCfg84:  // products without the SwiGLU epilogue only (with it, four
-                      // tiles per wave of two matrices spill registers)
+        case kCfg84:  // products without the SwiGLU epilogue only (it is never
+                      // chosen with it, and several tiles per wave of two
+                      // matrices spilled registers)
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg84, SWIGLU, XF32>(p, s);
             return hipErrorInvalidValue;
         case kCfg161:  // chosen for small products without the SwiGLU epilogue only

@@ -13,6 +13,10 @@
 //
 //   product (TILED)                          fp32 x in           quantized x in
 //   q/k/v 6144+1024+1024 x 5120 Q4_K         (8,4)  7.00 us      (4,1) 6.69 us
+//     (later, in graphs of 32 launches: (8,4,2) 5.95, (8,2,2) 5.96,
+//     (8,4,4) 6.00, (16,4,4) 6.39, (4,4,2) 6.54, (4,4,4) 7.20, (8,2,1) 7.37;
+//     the layer 0.45 us faster with (8,4,2) in two sessions; at M = 2 q/k/v
+//     7.8 against 8.4)
 //   o 5120 x 6144 Q4_K                       (8,2,2) 7.51 us     (8,1) 6.01 us
 //                                            (8,1) 7.88, (6,2,1) 7.98, (4,2,2) 8.24
 //   gate/up SwiGLU 2 x 17408 x 5120 Q4_K     (4,1) 20.91 us      (8,1) 20.19 us
@@ -68,7 +72,7 @@ struct GemvCfg {
 #define M27Q_CFG_42 4, 2, 2
 #endif
 #ifndef M27Q_CFG_84
-#define M27Q_CFG_84 8, 4, 4
+#define M27Q_CFG_84 8, 4, 2
 #endif
 #ifndef M27Q_CFG_Q
 #define M27Q_CFG_Q 2, 4, 2

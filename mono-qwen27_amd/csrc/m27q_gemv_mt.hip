@@ -189,7 +189,7 @@ static hipError_t launch_mt_cfg(MatmulMultiParams p, hipStream_t s) {
     return hipSuccess;
 }
 
-// Launch shape, from sweeps of the Qwen-27B layer at M = 2 and 4: (8, 4, 4)
+// Launch shape, from sweeps of the Qwen-27B layer at M = 2 and 4: (8, 4, 2)
 // for q/k/v (8192 rows of 20 units), (8, 1, 1) for o (24 units) and down (68
 // units), (4, 2, 2) for gate/up (34816 rows).
 static int pick_mt_cfg(long long rows, int upr) {
