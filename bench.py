@@ -12,7 +12,10 @@ kernel.  A step is one such layer pass.  Weights rotate over enough distinct
 device copies (>= 2 x the 256 MB Infinity Cache) that every step streams its
 weights from HBM; a warm (cache-resident) figure is reported beside it.  The
 passes replay from HIP graphs of 32 layer passes each, as a decode step
-replays one graph for all its layers.
+replays one graph for all its layers.  Before the W warmup passes, 100 ms of
+untimed layer passes let the GPU's clocks settle; each product timed alone
+rotates over copies of its own weights (>= 2 x the Infinity Cache) after 30 ms
+of untimed replays.
 
 value = weight bytes of the layer (GGUF, unpadded: 214,671,360 B) / step time.
 """
@@ -66,6 +69,22 @@ def build_layers(m27q, ora, dev, copies):
     return layers, host
 
 
+def cold_pool(m27q, torch, layers, names):
+    """Copies of the named weights, enough of them (>= 2 x the 256 MB Infinity
+    Cache per rotation, and at least the layer copies) that every launch of a
+    product timed alone streams its weights from HBM: the layer copies first,
+    then device clones of them."""
+    per = sum(layers[0][n].data.numel() for n in names)
+    n = max(len(layers), -(-2 * MALL_BYTES // per) + 1)
+    pool = [{k: L[k] for k in names} for L in layers]
+    while len(pool) < n:
+        src = layers[len(pool) % len(layers)]
+        pool.append({k: m27q.Weight(src[k].data.clone(), src[k].type, src[k].rb, src[k].rc, src[k].layout)
+                     for k in names})
+    torch.cuda.synchronize()
+    return pool
+
+
 class Buffers:
     def __init__(self, m27q, dev):
         import torch
@@ -89,7 +108,8 @@ STAGES = {
     "gate_up": lambda m27q, L, B, s: m27q.ffn_swiglu(L["gate"], L["up"], B.h, B.f, stream=s),
     "down": lambda m27q, L, B, s: m27q.matvec(L["down"], B.f, B.out, residual=B.h, stream=s),
 }
-STAGE_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
+STAGE_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",),
+                 "cfg1": ("gate",)}
 
 # Config 4: the same products on M quantized activation rows (A[K] holds the M
 # rows of length K; Y[name] is [M][rows]).
@@ -159,15 +179,32 @@ def rand_weight(m27q, torch, dev, t, rc, k, layout=None):
     return m27q.Weight(torch.from_numpy(host).to(dev), t, rb, rc, layout)
 
 
+SETTLE_MS = 30.0
+SETTLE_MS_LAYER = 100.0
+
+
+def settle(torch, g, ms=SETTLE_MS, min_replays=3):
+    """Untimed replays of g until the GPU has run it for at least ms.  After the
+    host has left the GPU idle (capturing graphs, cloning weights), its first
+    ~10 ms of work run slower: gate/up 20.4-21.2 us per launch against 18.4-19.0
+    once settled, the LM head 181 us against 163."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_replays or (time.perf_counter() - t0) * 1e3 < ms:
+        g.replay()
+        n += 1
+        if n % 2 == 0:
+            torch.cuda.synchronize()  # host time then tracks the GPU's
+    torch.cuda.synchronize()
+
+
 def timed(torch, fn, ncopies, reps, warm=3, calls=32):
     """Average us per call of fn(c, stream) over ncopies rotated inputs, captured in a
     graph of at least `calls` calls (whole rotations), so graph launch boundaries
-    stay rare; `warm` untimed replays first (the first replays after a stretch of
-    host work run measurably slower: 181 us against 163 for the LM head)."""
+    stay rare; at least `warm` untimed replays and SETTLE_MS of them first."""
     rot = max(1, -(-calls // ncopies))
     g = capture(torch, lambda st: [fn(c, st) for _ in range(rot) for c in range(ncopies)])
-    for _ in range(warm):
-        g.replay()
+    settle(torch, g, min_replays=warm)
     return time_graph(torch, g, max(1, reps // rot)) / (rot * ncopies) * 1e3
 
 
@@ -182,8 +219,9 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
     # config 1: Q4_K 17408 x 5120 alone, fp32 x
     if "cfg1" in sections:
         y = torch.empty(17408, dtype=torch.float32, device=dev)
-        us = timed(torch, lambda c, st: m27q.matvec(layers[c % len(layers)]["gate"], x5120, y, stream=st),
-                   len(layers), reps)
+        pool = cold_pool(m27q, torch, layers, STAGE_WEIGHTS["cfg1"])
+        us = timed(torch, lambda c, st: m27q.matvec(pool[c]["gate"], x5120, y, stream=st), len(pool), reps)
+        del pool
         out["cfg1_q4k_17408x5120_m1"] = {"us": round(us, 3), "GBps": round(50135040 / us / 1e3, 1)}
         log(f"config 1: {us:.2f} us")
     # config 2: Q8_0 draft shapes, fp32 x
@@ -336,8 +374,7 @@ def stream_read_peak(torch, dev, reps):
                     rc = L.m27q_stream_read(buf.data_ptr() + c * nbytes, nbytes, sink.data_ptr(), st.cuda_stream)
                     assert rc == 0, rc
         g = capture(torch, body)
-        for _ in range(3):
-            g.replay()
+        settle(torch, g)
         us = time_graph(torch, g, max(3, reps // 10)) / (per * ncopy) * 1e3
         out[f"{mb:g}MB"] = round(nbytes / us / 1e3, 1)
         log(f"stream read {mb:g} MB: {us:.2f} us, {out[f'{mb:g}MB']} GB/s")
@@ -411,6 +448,7 @@ def wave_timeline(m27q, torch, dev, layers, B, trials=3):
     N = 1 << 16
     q = lambda a: "/".join(f"{np.percentile(a, p):.2f}" for p in (0, 10, 50, 90, 100))
     for name, fn in prods.items():
+        pool = cold_pool(m27q, torch, layers, STAGE_WEIGHTS[name])
         for trial in range(trials):
             if L.m27q_timeline_clear() != 0:
                 raise RuntimeError("m27q_timeline_clear failed")
@@ -419,8 +457,8 @@ def wave_timeline(m27q, torch, dev, layers, B, trials=3):
             # or an idle queue starts its waves on the 8 XCDs up to ~4 us
             # apart, one that follows a kernel within ~0.2 us.  Every launch
             # writes the same slots, so the records are the last launch's.
-            for r in range(2 * len(layers) + trial + 1):
-                fn(m27q, layers[r % len(layers)], B, None)
+            for r in range(len(pool) + trial + 1):
+                fn(m27q, pool[r % len(pool)], B, None)
             torch.cuda.synchronize()
             t = np.zeros((N, 3), np.uint64)
             hw = np.zeros((N, 3), np.uint32)
@@ -528,6 +566,9 @@ def main():
         for c in range(r % copies):
             g_one[c].replay()
 
+    # The GPU's clocks settle first (untimed layer passes, SETTLE_MS_LAYER of
+    # them), then the W warmup passes run, then the K timed ones.
+    settle(torch, g_big, SETTLE_MS_LAYER)
     run_steps(args.warmup)
     torch.cuda.synchronize()
     log(f"timing {args.steps} layer passes")
@@ -548,14 +589,17 @@ def main():
     nb = max(1, greps // 4)
     per = [time_graph(torch, g_big, nb) / PG * 1e3 for _ in range(10)]
 
-    # Each product on its own, over the same rotated copies (ROT rotations per
-    # graph): average launch duration from HIP events on the replay stream.
+    # Each product on its own, over copies of its own weights that exceed the
+    # Infinity Cache twice over (graphs of at least 32 launches): average launch
+    # duration from HIP events on the replay stream.
     stages = {}
     for name, fn in STAGES.items():
-        g = capture(torch, lambda st, fn=fn: [fn(m27q, L, B, st) for _ in range(ROT) for L in layers])
-        for _ in range(3):
-            g.replay()
-        ms = time_graph(torch, g, greps) / PG
+        pool = cold_pool(m27q, torch, layers, STAGE_WEIGHTS[name])
+        rot = max(1, -(-32 // len(pool)))
+        g = capture(torch, lambda st, fn=fn: [fn(m27q, L, B, st) for _ in range(rot) for L in pool])
+        settle(torch, g)
+        ms = time_graph(torch, g, max(3, args.steps // (rot * len(pool)))) / (rot * len(pool))
+        del g, pool
         nbytes = stage_bytes(m27q, name)
         stages[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
         log(f"{name}: {ms * 1e3:.2f} us, {stages[name]['GBps']} GB/s")
@@ -592,7 +636,8 @@ def main():
         "config": {"workload": "qwen27b_q4km_decode_layer_linears_m1",
                    "layer": {n: f"{t} {rc}x{k}" for n, t, rc, k in LAYER},
                    "weight_bytes": layer_bytes, "layout": "tiled", "activation": "int8 per-32, fp32 scale",
-                   "cold_copies": copies, "graph": True, "layer_passes_per_graph": PG},
+                   "cold_copies": copies, "graph": True, "layer_passes_per_graph": PG,
+                   "untimed_settle_ms_before_warmup": SETTLE_MS_LAYER},
         "us_per_layer": round(ms_cold * 1e3, 2),
         "us_per_layer_batches_p10_median_p90": [round(float(np.percentile(per, q)), 2) for q in (10, 50, 90)],
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),

@@ -67,7 +67,20 @@ __device__ __forceinline__ uint4 ld_u128_a2(const uint8_t *p) {
     return make_uint4(ld_u32_a2(p), ld_u32_a2(p + 4), ld_u32_a2(p + 8), ld_u32_a2(p + 12));
 }
 
-__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) { return *(const uint4 *)p; }
+// 16-byte load.  NT marks it non-temporal (global_load_dwordx4 ... nt), the
+// policy of the weight streams, which are read once per product: it keeps them
+// from displacing the activations and outputs other workgroups and the next
+// launch read from the caches.
+template <bool NT = false>
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
+    if constexpr (NT) {
+        typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+        const u4v v = __builtin_nontemporal_load((const u4v *)p);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *(const uint4 *)p;
+    }
+}
 
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask, int width = kWave) {

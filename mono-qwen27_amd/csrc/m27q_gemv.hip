@@ -207,8 +207,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     const int rc = p.rc[m];
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
     // Tiles of this workgroup: TPW from tile0, or, with balanced tiling, nt
-    // of them (TPW - 1 or TPW); the slots past nt reread the workgroup's last
-    // tile (cache hits) and their rows are not written.
+    // of them (TPW - 1 or TPW); the waves of the slots past nt stream no
+    // units (their loads would go to HBM again: the weight loads are
+    // non-temporal) and those rows are not written.
     const int wg = (int)blockIdx.x - p.wg_start[m];
     int tile0 = wg * TPW, nt = TPW;
     if (p.bal) {
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     // valid unit and discards it.
     const int U = p.upr / KS, rem = p.upr % KS;
     const int ub = ks * U + min(ks, rem);
-    const int nu = U + (ks < rem ? 1 : 0);
+    const int nu = tg * WT >= nt ? 0 : U + (ks < rem ? 1 : 0);
 
     // 1. first batch of the activation, 2. the first unit of weights (their
     // latency overlaps the staging), 3. activation to LDS.
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     const uint8_t *W[NM];
     W[0] = p.W[m];
     if constexpr (SWIGLU) W[NM - 1] = p.W[1];
-    const UnitStream<T, LAYOUT, NM, WT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, p.rb, p.upr, lane);
+    const UnitStream<T, LAYOUT, NM, WT, C::NT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, p.rb, p.upr, lane);
     typename T::Frag fa[NM][WT], fb[NM][WT];
     ws.load(fa, min(ub, p.upr - 1));
 

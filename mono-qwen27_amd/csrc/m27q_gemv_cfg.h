@@ -4,6 +4,16 @@
 //  TPW : 8-row tiles per workgroup
 //  WT  : tiles per wave (TPW / WT tile groups), so a workgroup has
 //        NW = KS * TPW / WT wavefronts
+//  NT  : 1 = non-temporal weight loads (global_load_dwordx4 ... nt)
+//
+// Non-temporal weight loads were measured per shape, every product on cold
+// weights: gate/up 18.6-19.0 us against 20.2, down 16.5-16.8 against 17.9,
+// config 1 11.1 against 12.0, the LM head 152 against 164; q/k/v and o were
+// 0.3-0.6 us faster alone with them, but the decode layer (q/k/v, o, gate/up,
+// down in one graph) was 0.4-0.6 us slower with them on q/k/v and 0.3-0.7 us
+// slower with them on o, in two sessions, so those two shapes keep temporal
+// loads.  With the choices below the layer took 46.3-46.6 us against 50.2-50.4
+// with temporal loads everywhere.
 //
 // More, shorter wavefronts stream HBM better, but every workgroup stages (and,
 // for fp32 input, quantizes) the whole activation, so the best shape depends
@@ -55,36 +65,37 @@
 
 namespace m27q {
 
-template <int KS_, int TPW_, int WT_>
+template <int KS_, int TPW_, int WT_, int NT_ = 1>
 struct GemvCfg {
     static constexpr int KS = KS_, TPW = TPW_, WT = WT_, NW = KS_ * TPW_ / WT_;
+    static constexpr bool NT = NT_ != 0;  // non-temporal weight loads
     static_assert(KS >= 1 && TPW >= 1 && WT >= 1 && TPW % WT == 0, "bad GEMV configuration");
     static_assert(NW >= 1 && NW <= 16, "a workgroup holds at most 16 wavefronts");
 };
 
 #ifndef M27Q_CFG_41
-#define M27Q_CFG_41 4, 1, 1
+#define M27Q_CFG_41 4, 1, 1, 1
 #endif
 #ifndef M27Q_CFG_81
-#define M27Q_CFG_81 8, 1, 1
+#define M27Q_CFG_81 8, 1, 1, 1
 #endif
 #ifndef M27Q_CFG_42
-#define M27Q_CFG_42 4, 2, 2
+#define M27Q_CFG_42 4, 2, 2, 1
 #endif
 #ifndef M27Q_CFG_84
-#define M27Q_CFG_84 8, 4, 2
+#define M27Q_CFG_84 8, 4, 2, 0
 #endif
 #ifndef M27Q_CFG_Q
-#define M27Q_CFG_Q 2, 4, 2
+#define M27Q_CFG_Q 2, 4, 2, 1
 #endif
 #ifndef M27Q_CFG_161
-#define M27Q_CFG_161 16, 1, 1
+#define M27Q_CFG_161 16, 1, 1, 1
 #endif
 #ifndef M27Q_CFG_822
-#define M27Q_CFG_822 8, 2, 2
+#define M27Q_CFG_822 8, 2, 2, 0
 #endif
 #ifndef M27Q_CFG_B
-#define M27Q_CFG_B 4, 3, 1
+#define M27Q_CFG_B 4, 3, 1, 1
 #endif
 
 using Cfg41 = GemvCfg<M27Q_CFG_41>;

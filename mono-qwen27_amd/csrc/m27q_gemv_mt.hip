@@ -35,8 +35,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     const int rc = p.rc[mi];
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
     // Tiles of this workgroup: TPW from tile0, or, with balanced tiling, nt
-    // of them (TPW - 1 or TPW); the slots past nt reread the workgroup's last
-    // tile (cache hits) and their rows are not written.
+    // of them (TPW - 1 or TPW); the waves of the slots past nt stream no
+    // units (their loads would go to HBM again: the weight loads are
+    // non-temporal) and those rows are not written.
     const int wg = (int)blockIdx.x - p.wg_start[mi];
     int tile0 = wg * TPW, nt = TPW;
     if (p.bal_wgs > 0) {
@@ -45,11 +46,11 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     }
     const int U = p.upr / KS, rem = p.upr % KS;
     const int ub = ks * U + min(ks, rem);
-    const int nu = U + (ks < rem ? 1 : 0);
+    const int nu = tg * WT >= nt ? 0 : U + (ks < rem ? 1 : 0);
 
     // First unit of weights before the staging, so their latencies overlap.
     const uint8_t *W[1] = {p.W[mi]};
-    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, 0, p.upr, lane);
+    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT, C::NT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, 0, p.upr, lane);
     typename T::Frag fa[1][WT], fb[1][WT];
     ws.load(fa, min(ub, p.upr - 1));
 

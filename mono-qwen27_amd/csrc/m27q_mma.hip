@@ -79,9 +79,16 @@ __device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// AUX is the cache policy: 2 marks the load non-temporal (buffer_load ... nt),
+// the policy of the weight streams, which are read once per product.
+template <int AUX = 0>
 __device__ __forceinline__ v4u buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
 }
+#ifndef M27Q_MMA_NT
+#define M27Q_MMA_NT 1
+#endif
+constexpr int kWeightAux = M27Q_MMA_NT ? 2 : 0;
 __device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
 __device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
 __device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
@@ -577,7 +584,7 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     uint32_t ss[4] = {0u, 0u, 0u, 0u};
     auto issue = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) rw[n] = buf_ld16(wr, goff[n], (uint32_t)u * UB);
+        for (int n = 0; n < SG::kNW; ++n) rw[n] = buf_ld16<kWeightAux>(wr, goff[n], (uint32_t)u * UB);
 #pragma unroll
         for (int n = 0; n < SG::kNA; ++n) ra[n] = buf_ld16(xr, aoff[n], (uint32_t)u * UE);
         if constexpr (G == 8) {  // whole units: rows of 8 k groups, 16-byte aligned
@@ -814,7 +821,7 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
 #pragma unroll
         for (int n = 0; n < SG::kNW; ++n) {
             const int tile = min(tile0 + wt[n], ntiles8 - 1);
-            rw[n] = buf_ld16(wr, (uint32_t)tile * (uint32_t)(upr * UB) + 16u * (uint32_t)wc[n], (uint32_t)u * UB);
+            rw[n] = buf_ld16<kWeightAux>(wr, (uint32_t)tile * (uint32_t)(upr * UB) + 16u * (uint32_t)wc[n], (uint32_t)u * UB);
         }
     };
     auto commit = [&]() __attribute__((always_inline)) {

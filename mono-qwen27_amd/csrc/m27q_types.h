@@ -85,12 +85,14 @@ struct Q4K {
         float dsum;
     };
 
+    template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
-        return {ld_u128(unit + 128 + 128 * i + 16 * c), ld_u128(unit + 16 * i)};
+        return {ld_u128<NT>(unit + 128 + 128 * i + 16 * c), ld_u128<NT>(unit + 16 * i)};
     }
+    template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
         const uint8_t *blk = row + (size_t)u * kQ4KBytes;
-        return {ld_u128(blk + kQ4KHdr + 16 * c), ld_u128(blk)};
+        return {ld_u128<NT>(blk + kQ4KHdr + 16 * c), ld_u128<NT>(blk)};
     }
 
     // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c.
@@ -185,13 +187,15 @@ struct Q5K : Q4K {
         uint4 h;   // d | dmin << 16, scales[12]
     };
 
+    template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
-        return {ld_u128(unit + 128 + 128 * i + 16 * c), ld_u128(unit + kQ5KTQh + 32 * i + 16 * (c & 1)),
-                ld_u128(unit + 16 * i)};
+        return {ld_u128<NT>(unit + 128 + 128 * i + 16 * c), ld_u128<NT>(unit + kQ5KTQh + 32 * i + 16 * (c & 1)),
+                ld_u128<NT>(unit + 16 * i)};
     }
+    template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
         const uint8_t *blk = row + (size_t)u * kQ5KBytes;
-        return {ld_u128(blk + kQ5KQs + 16 * c), ld_u128(blk + kQ5KQh + 16 * (c & 1)), ld_u128(blk)};
+        return {ld_u128<NT>(blk + kQ5KQs + 16 * c), ld_u128<NT>(blk + kQ5KQh + 16 * (c & 1)), ld_u128<NT>(blk)};
     }
 
     // 5-bit codes of one dword: the nibbles plus bit 2g (low) / 2g + 1 (high)
@@ -275,15 +279,17 @@ struct Q6K {
         }
     };
 
+    template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &L) {
         Frag f;
-        f.ql = ld_u128(unit + kQ6KTQl + 128 * i + 16 * c);
-        f.qh = ld_u128(unit + kQ6KTQh + 64 * i + L.qh_off);
+        f.ql = ld_u128<NT>(unit + kQ6KTQl + 128 * i + 16 * c);
+        f.qh = ld_u128<NT>(unit + kQ6KTQh + 64 * i + L.qh_off);
         f.sc = *(const uint2 *)(unit + kQ6KTSc + 16 * i + 8 * L.hh);
         f.d = *(const uint32_t *)(unit + kQ6KTD + 4 * (i >> 1));  // the d pair of rows i & ~1, i | 1
         f.dsh = 16 * (i & 1);
         return f;
     }
+    template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &L) {
         const uint8_t *blk = row + (size_t)u * kQ6KBytes;
         Frag f;
@@ -403,9 +409,11 @@ struct IQ4XS {
         float dx;
     };
 
+    template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
-        return {ld_u128(unit + 128 * i + 16 * c), *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i)};
+        return {ld_u128<NT>(unit + 128 * i + 16 * c), *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i)};
     }
+    template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
         const uint8_t *blk = row + (size_t)u * kIQ4XSBytes;
         const uint2 a = *(const uint2 *)(blk + kIQ4XSQs + 16 * c), b = *(const uint2 *)(blk + kIQ4XSQs + 16 * c + 8);
@@ -476,9 +484,11 @@ struct Q80 {
         __device__ explicit Lane(int c) : k(c >> 1), hf(c & 1) {}
     };
 
+    template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int /*c*/, const Lane &L) {
-        return {ld_u128(unit + 128 * i + 32 * L.k + 16 * L.hf), *(const uint16_t *)(unit + kQ80TD + 8 * i + 2 * L.k)};
+        return {ld_u128<NT>(unit + 128 * i + 32 * L.k + 16 * L.hf), *(const uint16_t *)(unit + kQ80TD + 8 * i + 2 * L.k)};
     }
+    template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int rb, int /*c*/, const Lane &L) {
         const int bi = 4 * u + L.k;
         if (bi >= rb) return {make_uint4(0, 0, 0, 0), 0u};
@@ -526,7 +536,7 @@ struct Q80 {
 // ------------------------------------------------------- weight stream --
 // Weight fragments of one unit for the TPW tiles of every matrix (the caller
 // includes m27q.h for the layout tags).
-template <class T, int LAYOUT, int NM, int TPW>
+template <class T, int LAYOUT, int NM, int TPW, bool NT = false>
 struct UnitStream {
     const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
     int i, c, rb;
@@ -554,9 +564,9 @@ struct UnitStream {
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
                 if constexpr (LAYOUT == M27Q_LAYOUT_TILED)
-                    f[m][t] = T::load_tiled(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
+                    f[m][t] = T::template load_tiled<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
                 else
-                    f[m][t] = T::load_gguf(base[m][t], u, rb, c, L);
+                    f[m][t] = T::template load_gguf<NT>(base[m][t], u, rb, c, L);
             }
     }
 };
