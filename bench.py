@@ -266,9 +266,12 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
         # 16 calls per graph replay, so the host's replay cost stays hidden behind the GPU
         us = timed(torch, lambda c, st: m27q.topk(logits, k, idx, val, scratch, stream=st), 16, reps)
         out["cfg5_topk64_of_248320"] = {"us": round(us, 3), "GBps": round(248320 * 4 / us / 1e3, 1)}
-        ids = [torch.from_numpy(rng.integers(0, 248320, 512).astype(np.int32)).to(dev) for _ in range(16)]
+        # 256 id sets (2.15 MB of rows each, 550 MB over a rotation: >= 2 x the
+        # Infinity Cache), so the rows stream from HBM as in a cold prefill
+        nsets = -(-2 * MALL_BYTES // (512 * 4200)) + 1
+        ids = [torch.from_numpy(rng.integers(0, 248320, 512).astype(np.int32)).to(dev) for _ in range(nsets)]
         rows = torch.empty((512, 5120), dtype=torch.float32, device=dev)
-        us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids[c], rows, stream=st), 16, reps)
+        us = timed(torch, lambda c, st: m27q.embed_rows(lm, ids[c], rows, stream=st), nsets, reps)
         out["cfg5_gather_512_q6k_rows"] = {"us": round(us, 3),
                                            "GBps": round((512 * 4200 + 512 * 5120 * 4) / us / 1e3, 1)}
         log("config 5 done")

@@ -2,6 +2,7 @@
 argument validation (every check returns before the first HIP call, so bogus
 device pointers are never dereferenced here)."""
 import ctypes as C
+import os
 import subprocess
 
 import numpy as np
@@ -208,3 +209,18 @@ def test_validation_gather_and_topk(m27q):
     assert L.m27q_sample(FAKE, FAKE, 40, 1.0, 0.05, 0.0, FAKE, FAKE, None) == 6
     assert L.m27q_sample(None, FAKE, 40, 1.0, 0.05, 0.9, FAKE, FAKE, None) == 1
     assert m27q.topk_scratch_bytes(10, 11) == 0
+
+
+C_CALLER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c_abi", "_build", "abi_caller")
+
+
+def test_c_caller_cpu(m27q):
+    """A C99 program that includes include/m27q.h and links libm27q.so (as the
+    reference's host code would) runs the host-side entry points and the host
+    validation of the device entry points."""
+    if not os.path.exists(C_CALLER):
+        subprocess.run(["make", "-C", os.path.dirname(os.path.dirname(C_CALLER))], check=True,
+                       capture_output=True)
+    r = subprocess.run([C_CALLER, "--cpu"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "abi_caller: ok" in r.stdout
