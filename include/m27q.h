@@ -303,7 +303,7 @@ M27Q_API m27q_status m27q_topk(const float *logits, int n, int k, int32_t *idx, 
 /* m27q_topk without a scratch argument: no counterpart in the reference; for
  * callers that cannot allocate device memory (code under graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The library keeps the
- * scratch in a static device array of m27q_topk_scratch_bytes (133,128 bytes;
+ * scratch in a static device array of m27q_topk_scratch_bytes (134,144 bytes;
  * n <= 2^24) per device, held until the process ends; n beyond that returns
  * M27Q_ERR_SCRATCH before any launch.  The first call on a device resolves
  * the array's address (hipGetSymbolAddress), so make it outside graph

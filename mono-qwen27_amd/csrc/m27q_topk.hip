@@ -10,15 +10,16 @@
 //   1. chunk maxima: workgroup c writes the largest key of its chunk;
 //   2. filter: every workgroup takes T = the k-th largest chunk maximum (k
 //      chunks hold a key >= T, so the k-th largest key overall is >= T) and
-//      appends the keys >= T of its chunk to a candidate list, reserving its
-//      slots with one atomic on a counter;
+//      writes the keys >= T of its chunk to the chunk's own k candidate slots,
+//      and their count beside them (no atomic across workgroups: one counter
+//      serialized the workgroups' reservations);
 //      A chunk with more than k such keys first reduces them to its own top k
-//      (radix select within the workgroup), so the list never exceeds
-//      nchunks * k keys;
-//   3. select (one workgroup): with at most 1024 candidates (the usual case:
-//      about 75 for 248320 i.i.d. logits) each candidate's rank is counted
-//      directly and the first k are written in rank order; with more, a radix
-//      select runs over the candidates.
+//      (radix select within the workgroup);
+//   3. select (one workgroup): the chunks' counts give each candidate its
+//      place; with at most 1024 candidates (the usual case: about 75 for
+//      248320 i.i.d. logits) each candidate's rank is counted directly and the
+//      first k are written in rank order; with more, a radix select runs over
+//      the candidate slots.
 // Replaces the CPU selection of sample() (src/mono27b_chat.cpp:211-227) and
 // k_argmax (exec:211-239).
 #include <atomic>
@@ -49,26 +50,39 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// Scratch layout: chunk maxima, the candidate counter, the candidates.
+// Scratch layout: chunk maxima, each chunk's candidate count, each chunk's k
+// candidate slots (chunk c: cand[c * k .. c * k + count[c])).
 struct TopkScratch {
     uint64_t *maxkey;  // [kTopkMaxChunks]
-    uint32_t *count;   // one counter (8-byte slot)
+    uint32_t *count;   // [kTopkMaxChunks]
     uint64_t *cand;    // [kTopkCap]
 };
+constexpr size_t kTopkScratchWords = (size_t)kTopkMaxChunks + kTopkMaxChunks / 2 + kTopkCap;
 __host__ __device__ inline TopkScratch topk_scratch(void *base) {
     uint64_t *p = (uint64_t *)base;
-    return {p, (uint32_t *)(p + kTopkMaxChunks), p + kTopkMaxChunks + 1};
+    return {p, (uint32_t *)(p + kTopkMaxChunks), p + kTopkMaxChunks + kTopkMaxChunks / 2};
 }
 
-// 1. Largest key of each chunk; workgroup 0 also clears the counter (the
-// launches run in stream order, so the filter sees it cleared).
+// 1. Largest key of each chunk.
 __global__ __launch_bounds__(kTopkBlock) void k_topk_chunk_max(const float *__restrict__ v, int n, int chunk,
                                                                TopkScratch sc) {
     __shared__ uint64_t wmax[kTopkBlock / kWave];
     const long long base = (long long)blockIdx.x * chunk;
     const int end = (int)min((long long)n, base + chunk);
     uint64_t m = 0;
-    for (int i = (int)base + (int)threadIdx.x; i < end; i += kTopkBlock) {
+    // four independent loads per thread and round (a chunk of 1024 is one round)
+    int i = (int)base + (int)threadIdx.x;
+    for (; i + 3 * kTopkBlock < end; i += 4 * kTopkBlock) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = v[i + u * kTopkBlock];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint64_t key = topk_key(x[u], (uint32_t)(i + u * kTopkBlock));
+            m = key > m ? key : m;
+        }
+    }
+    for (; i < end; i += kTopkBlock) {
         const uint64_t key = topk_key(v[i], (uint32_t)i);
         m = key > m ? key : m;
     }
@@ -84,7 +98,6 @@ __global__ __launch_bounds__(kTopkBlock) void k_topk_chunk_max(const float *__re
 #pragma unroll
         for (int w = 1; w < kTopkBlock / kWave; ++w) r = wmax[w] > r ? wmax[w] : r;
         sc.maxkey[blockIdx.x] = r;
-        if (blockIdx.x == 0) *sc.count = 0u;
     }
 }
 
@@ -201,17 +214,25 @@ __device__ void block_select_stream(Get get, int count, int k, uint64_t *out, Se
     __syncthreads();
 }
 
-// 2. Keys >= T of each chunk onto the candidate list.  A chunk with more than
-// k of them (ties, sorted input) contributes only its own top k, so the list
-// holds at most nchunks * k <= kTopkCap keys.
+// 2. Keys >= T of each chunk into its k candidate slots.  A chunk with more
+// than k of them (ties, sorted input) contributes only its own top k.
 __global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restrict__ v, int n, int k, int chunk,
                                                             int nchunks, TopkScratch sc) {
     __shared__ uint64_t mk[kTopkMaxChunks];
     __shared__ uint64_t bound;
-    __shared__ uint32_t local, gbase;
+    __shared__ uint32_t local;
     __shared__ SelectShared sh;
     __shared__ uint64_t best[kTopkMaxK];
     const int t = (int)threadIdx.x;
+    const int base = (int)blockIdx.x * chunk;
+    const int len = min(n - base, chunk);
+    // The chunk's first 4 x 256 values, loaded while T is found.
+    float x0[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = t + u * kTopkBlock;
+        x0[u] = i < len ? v[base + i] : 0.f;
+    }
     if (t < nchunks) mk[t] = sc.maxkey[t];
     if (t == 0) {
         bound = 0ull;  // fewer than k chunks: no bound
@@ -226,11 +247,15 @@ __global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restr
     }
     __syncthreads();
     const uint64_t T = bound;
-    const int base = (int)blockIdx.x * chunk;
-    const int len = min(n - base, chunk);
     // Count, reserve, write (the chunk is L2-resident after the first sweep).
     uint32_t mine = 0;
-    for (int i = t; i < len; i += kTopkBlock) mine += topk_key(v[base + i], (uint32_t)(base + i)) >= T;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = t + u * kTopkBlock;
+        mine += i < len && topk_key(x0[u], (uint32_t)(base + i)) >= T;
+    }
+    for (int i = t + 4 * kTopkBlock; i < len; i += kTopkBlock)
+        mine += topk_key(v[base + i], (uint32_t)(base + i)) >= T;
     if (mine) atomicAdd(&local, mine);
     __syncthreads();
     const uint32_t found = local;
@@ -242,19 +267,24 @@ __global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restr
                 return key >= T ? key : 0ull;
             },
             len, k, best, sh);
-        if (t == 0) gbase = atomicAdd(sc.count, (uint32_t)k);
-        __syncthreads();
-        if (t < k) sc.cand[gbase + t] = best[t];
+        if (t < k) sc.cand[(size_t)blockIdx.x * k + t] = best[t];
+        if (t == 0) sc.count[blockIdx.x] = (uint32_t)k;
         return;
     }
     if (t == 0) {
-        gbase = found ? atomicAdd(sc.count, found) : 0u;
+        sc.count[blockIdx.x] = found;
         local = 0u;
     }
     __syncthreads();
     if (!mine) return;
-    uint32_t off = gbase + atomicAdd(&local, mine);
-    for (int i = t; i < len; i += kTopkBlock) {
+    uint32_t off = (uint32_t)blockIdx.x * (uint32_t)k + atomicAdd(&local, mine);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = t + u * kTopkBlock;
+        const uint64_t key = topk_key(x0[u], (uint32_t)(base + i));
+        if (i < len && key >= T) sc.cand[off++] = key;
+    }
+    for (int i = t + 4 * kTopkBlock; i < len; i += kTopkBlock) {
         const uint64_t key = topk_key(v[base + i], (uint32_t)(base + i));
         if (key >= T) sc.cand[off++] = key;
     }
@@ -281,18 +311,48 @@ __device__ __forceinline__ void topk_emit(const float *v, uint64_t key, int rank
     val[rank] = v[id];  // the original bits (keeps -0.0 and NaN payloads)
 }
 
-// 3. The top k of the candidates (k <= count <= nchunks * k).
-__global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__restrict__ v, int k, TopkScratch sc,
-                                                               int32_t *__restrict__ idx, float *__restrict__ val) {
+// 3. The top k of the candidates (k <= their number <= nchunks * k).
+__global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__restrict__ v, int k, int nchunks,
+                                                               TopkScratch sc, int32_t *__restrict__ idx,
+                                                               float *__restrict__ val) {
     __shared__ uint64_t keys[kTopkSelBlock];
+    __shared__ uint32_t cnt[kTopkMaxChunks], start[kTopkMaxChunks];
+    __shared__ int total_s;
     __shared__ SelectShared sh;
     __shared__ uint64_t best[kTopkMaxK];
     const int t = (int)threadIdx.x;
-    const int total = (int)*sc.count;
+    if (t < kTopkMaxChunks) cnt[t] = t < nchunks ? sc.count[t] : 0u;
+    __syncthreads();
+    if (t < kWave) {  // exclusive prefix of the counts, 4 chunks per lane
+        uint32_t c[4], s4 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = cnt[4 * t + i];
+            s4 += c[i];
+        }
+        uint32_t incl = s4;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d, kWave);
+            if (t >= d) incl += o;
+        }
+        uint32_t run = incl - s4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            start[4 * t + i] = run;
+            run += c[i];
+        }
+        if (t == kWave - 1) total_s = (int)incl;
+    }
+    __syncthreads();
+    const int total = total_s;
     if (total <= kTopkSelBlock) {
-        const uint64_t me = t < total ? sc.cand[t] : 0ull;
-        keys[t] = me;
+        keys[t] = 0ull;
         __syncthreads();
+        if (t < nchunks)
+            for (uint32_t i = 0; i < cnt[t]; ++i) keys[start[t] + i] = sc.cand[(size_t)t * k + i];
+        __syncthreads();
+        const uint64_t me = keys[t];
         if (t < total) {
             int rank = 0;
             for (int j = 0; j < total; ++j) rank += keys[j] > me;
@@ -301,7 +361,8 @@ __global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__re
         return;
     }
     const uint64_t *cand = sc.cand;
-    block_select_stream([&](int i) { return cand[i]; }, total, k, best, sh);
+    block_select_stream([&](int i) { return (uint32_t)(i % k) < cnt[i / k] ? cand[i] : 0ull; }, nchunks * k, k,
+                        best, sh);
     if (t < kWave) {
         const uint64_t s = wave_sort_desc(t < k ? best[t] : 0ull, t);
         if (t < k) topk_emit(v, s, t, idx, val);
@@ -390,17 +451,16 @@ int topk_max_n() { return (1 << 16) * kTopkMaxChunks; }
 
 size_t topk_scratch_bytes(int n) {
     if (!topk_chunk(n)) return 0;
-    return (size_t)(kTopkMaxChunks + 1 + kTopkCap) * sizeof(uint64_t);
+    return kTopkScratchWords * sizeof(uint64_t);
 }
 
 // The library's own top-k scratch for callers that cannot allocate
 // (m27q_topk_noalloc): one fixed-size array per device, held until the
 // process ends.  Host code never passes the array's name to a kernel: its
 // device address is resolved once per device with hipGetSymbolAddress and
-// cached.  Every call on a device shares that device's array (k_topk_chunk_max
-// clears the candidate counter in the array itself on every call), so calls
-// that overlap on one device race.
-constexpr size_t kTopkScratchWords = (size_t)kTopkMaxChunks + 1 + kTopkCap;
+// cached.  Every call on a device shares that device's array (every call
+// writes each chunk's maximum, count and candidates before they are read), so
+// calls that overlap on one device race.
 static __device__ __align__(256) uint64_t scratch[kTopkScratchWords];
 
 size_t topk_static_scratch_bytes() { return sizeof(scratch); }
@@ -433,7 +493,7 @@ hipError_t launch_topk(const float *v, int n, int k, int32_t *idx, float *val, v
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_topk_filter, dim3(nchunks), dim3(kTopkBlock), 0, s, v, n, k, chunk, nchunks, sc);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kTopkSelBlock), 0, s, v, k, sc, idx, val);
+    hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kTopkSelBlock), 0, s, v, k, nchunks, sc, idx, val);
     return hipGetLastError();
 }
 
