@@ -535,7 +535,9 @@ struct Q80 {
 
 // ------------------------------------------------------- weight stream --
 // Weight fragments of one unit for the TPW tiles of every matrix (the caller
-// includes m27q.h for the layout tags).
+// includes m27q.h for the layout tags).  NT selects non-temporal 16-byte loads
+// (ld_u128<true>); the GGUF blocks that are only 2- or 8-byte aligned (Q6_K,
+// Q8_0, IQ4_XS) are read in smaller pieces and keep the default policy.
 template <class T, int LAYOUT, int NM, int TPW, bool NT = false>
 struct UnitStream {
     const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
