@@ -133,7 +133,10 @@ struct Q4K {
         shi = dot4((int)((f.q.w >> 4) & kM4), a.hi.w, shi);
         return combine(f.h, a, L, slo, shi);
     }
-    // The scale terms of the lane's two 16-value halves from their integer sums.
+    // The scale terms of the lane's two 16-value halves from their integer sums
+    // (each 32-group is split over lanes c = 2g, 2g + 1, so its two halves are
+    // scaled apart and added in fp32; completing the group's integer sum first,
+    // with one DPP swap per pair, made config 1 0.5 us slower).
     __device__ static float combine(const uint4 &h, const AFrag &a, const Lane &L, int slo, int shi) {
         const uint32_t pair = scale_pair(h, L);
         const int m = min_c(h, L);
@@ -507,13 +510,16 @@ struct Q80 {
         return {*(const int4 *)(a.xc + 128 * u + 32 * L.k + 16 * L.hf), a.xd[4 * u + L.k]};
     }
 
-    // d_w dx sum(q q8) per block (vec_dot_q8_0_q8_1, exec:535-580), this lane's half.
-    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &) {
+    // d_w dx sum(q q8) per block (vec_dot_q8_0_q8_1, exec:535-580).  The two
+    // lanes of a block add their half sums (DPP) and the first scales the
+    // whole block, so each block's integer sum is complete before its scales.
+    __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
         int s = dot4((int)f.q.x, a.x.x, 0);
         s = dot4((int)f.q.y, a.x.y, s);
         s = dot4((int)f.q.z, a.x.z, s);
         s = dot4((int)f.q.w, a.x.w, s);
-        return f16_bits_to_f32(f.d) * (a.d * (float)s);
+        s += dpp_i<kDppXor1>(s);
+        return L.hf ? 0.f : f16_bits_to_f32(f.d) * (a.d * (float)s);
     }
     __device__ static float dot(const Frag &f, const ActLds &a, int u, const Lane &L) {
         return dot(f, load_act(a, u, L), L);

@@ -515,7 +515,12 @@ static int s16hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
  *      d*sc_j*dx_j*sum(q4*q8) - dmin*m_j*dx_j*sum(q8)
  *  Q6_K (exec:586-628): per 16-group j, d*sc_j*dx_(j/2)*sum((q6-32)*q8)
  *  Q8_0 (exec:535-580): per block b, d_w*dx_b*sum(q*q8)
- * Integer partial sums are exact; the fp64 combine has relative error ~1e-16. */
+ * Integer partial sums are exact; the fp64 combine has relative error ~1e-16.
+ * *norm is sum |term| over the pieces the GPU kernels scale one by one before
+ * adding in fp32 (the tests' fp32 error bound is relative to it): for Q4_K and
+ * Q5_K the main term of each 16-value half of a 32-group (the M = 1 and
+ * few-token kernels give each half to its own lane) and each group's min term;
+ * whole blocks for Q8_0, 16-value sub-blocks for Q6_K, 32-groups for IQ4_XS. */
 double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const float *d,
                    const uint32_t *s, double *norm) {
     double acc = 0.0, nrm = 0.0;
@@ -527,16 +532,17 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
                 uint8_t sc, m;
                 ora_get_scale_min_k4(j, w[b].scales, &sc, &m);
                 const int g = j / 2, hi = j & 1;
-                int sumi = 0;
+                int sumi = 0, half[2] = {0, 0};
                 for (int l = 0; l < 32; ++l) {
                     const int qw = hi ? (w[b].qs[32 * g + l] >> 4) : (w[b].qs[32 * g + l] & 15);
                     sumi += qw * q[256 * b + 32 * j + l];
+                    half[l >> 4] += qw * q[256 * b + 32 * j + l];
                 }
                 const int S = s16lo(s[8 * b + j]) + s16hi(s[8 * b + j]);
                 const double dx = d[8 * b + j];
                 const double t1 = dw * sc * dx * sumi, t2 = dm * m * dx * S;
                 acc += t1 - t2;
-                nrm += fabs(t1) + fabs(t2);
+                nrm += fabs(dw * sc * dx * half[0]) + fabs(dw * sc * dx * half[1]) + fabs(t2);
             }
         }
     } else if (type == ORA_Q5_K) {
@@ -548,17 +554,18 @@ double ora_dot_act(int type, const void *wrow, int rb, const int8_t *q, const fl
                 uint8_t sc, m;
                 ora_get_scale_min_k4(j, w[b].scales, &sc, &m);
                 const int g = j / 2, hi = j & 1;
-                int sumi = 0;
+                int sumi = 0, half[2] = {0, 0};
                 for (int l = 0; l < 32; ++l) {
                     const int nib = hi ? (w[b].qs[32 * g + l] >> 4) : (w[b].qs[32 * g + l] & 15);
                     const int qw = nib + (((w[b].qh[l] >> j) & 1) << 4);
                     sumi += qw * q[256 * b + 32 * j + l];
+                    half[l >> 4] += qw * q[256 * b + 32 * j + l];
                 }
                 const int S = s16lo(s[8 * b + j]) + s16hi(s[8 * b + j]);
                 const double dx = d[8 * b + j];
                 const double t1 = dw * sc * dx * sumi, t2 = dm * m * dx * S;
                 acc += t1 - t2;
-                nrm += fabs(t1) + fabs(t2);
+                nrm += fabs(dw * sc * dx * half[0]) + fabs(dw * sc * dx * half[1]) + fabs(t2);
             }
         }
     } else if (type == ORA_Q6_K) {
