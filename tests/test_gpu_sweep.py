@@ -6,11 +6,15 @@ remainders), fp32 or quantized activations, residual, multi-weight launches
 of mixed types and the SwiGLU epilogue.  The fixed cases elsewhere pin the
 benched shapes and the edges the kernels were written for; these cover the
 combinations between them (any layout, except multi-weight launches of
-several tokens, which take TILED weights)."""
+several tokens, which take TILED weights).  A second set of seeds draws the
+weights as random bytes in every field (6-bit scales and mins at their
+extremes, Q6_K's int8 scales down to -128, IQ4_XS's split scale bits, zero,
+subnormal and negative fp16 scales) instead of the quantizer's output."""
 import numpy as np
 import pytest
 
 from gpu_util import act_host, int_dot_tol, say, to_dev, to_host
+from test_oracle import random_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -27,21 +31,34 @@ def draw(seed):
                 fp32x=bool(r.integers(2)), res=bool(r.integers(2)), kind=int(r.integers(4)), r=r)
 
 
-def weight(m27q, ora, dev, t, rc, k, layout, seed):
+def weight(m27q, ora, dev, t, rc, k, layout, seed, raw=False):
+    """Quantizer-made blocks, or (raw) random bytes with finite fp16 scales."""
     tid = getattr(m27q, t)
-    wb = ora.synth_weights(tid, rc, k, seed=seed)
     rb = k // m27q.BLOCK_ELEMS[tid]
+    if raw:
+        wb = random_blocks(ora, tid, rb * rc, np.random.default_rng(7000 + seed))
+    else:
+        wb = ora.synth_weights(tid, rc, k, seed=seed)
     return tid, wb, rb, m27q.Weight.upload(wb.reshape(-1), tid, rb, rc, layout, dev)
 
 
 @pytest.mark.parametrize("seed", range(64))
 def test_random_product_vs_oracle(m27q, ora, dev, seed):
+    run_case(m27q, ora, dev, seed, raw=False)
+
+
+@pytest.mark.parametrize("seed", range(5000, 5032))
+def test_random_bytes_vs_oracle(m27q, ora, dev, seed):
+    run_case(m27q, ora, dev, seed, raw=True)
+
+
+def run_case(m27q, ora, dev, seed, raw):
     import torch
     c = draw(seed)
     t, k, rc, M, layout, r = c["type"], c["k"], c["rc"], c["M"], c["layout"], c["r"]
     if c["kind"] == 2 and M > 1:
         layout = m27q.TILED  # multi-weight small-M launches take TILED weights
-    tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, layout, seed)
+    tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, layout, seed, raw)
     X = r.standard_normal((M, k)).astype(np.float32)
     act = m27q.Act(M, k, dev)
     xd = to_dev(X, dev)
@@ -51,9 +68,9 @@ def test_random_product_vs_oracle(m27q, ora, dev, seed):
 
     if c["kind"] == 3 and M == 1:
         # SwiGLU: a second weight of the same type, shape and layout
-        _, ub, _, uw = weight(m27q, ora, dev, t, rc, k, layout, seed + 500)
+        _, ub, _, uw = weight(m27q, ora, dev, t, rc, k, layout, seed + 500, raw)
         y = torch.empty(rc, dtype=torch.float32, device=dev)
-        say("sweep swiglu", seed, t, rc, k, layout, "fp32 x" if c["fp32x"] else "q8 x")
+        say("sweep swiglu", "raw" if raw else "", seed, t, rc, k, layout, "fp32 x" if c["fp32x"] else "q8 x")
         if c["fp32x"]:
             m27q.ffn_swiglu(w, uw, xd.view(-1), y)
         else:
@@ -70,10 +87,10 @@ def test_random_product_vs_oracle(m27q, ora, dev, seed):
             if (ti == "Q8_0") != (t == "Q8_0") and k % 256:
                 ti = t  # K must be whole blocks of every type
             rci = int(r.integers(1, 3001))
-            tj, wbj, rbj, wj = weight(m27q, ora, dev, ti, rci, k, layout, seed + 100 * i)
+            tj, wbj, rbj, wj = weight(m27q, ora, dev, ti, rci, k, layout, seed + 100 * i, raw)
             mats.append((tj, wbj, rbj, wj, rci))
         Ys = [torch.empty((M, m[4]), dtype=torch.float32, device=dev) for m in mats]
-        say("sweep multi", seed, [(m[0], m[4]) for m in mats], k, M, layout)
+        say("sweep multi", "raw" if raw else "", seed, [(m[0], m[4]) for m in mats], k, M, layout)
         if M == 1 and c["fp32x"]:
             m27q.matvec_multi([m[3] for m in mats], xd.view(-1), [Y.view(-1) for Y in Ys])
         elif M == 1:
@@ -90,7 +107,7 @@ def test_random_product_vs_oracle(m27q, ora, dev, seed):
     res = r.standard_normal((M, rc)).astype(np.float32) if c["res"] else None
     resd = to_dev(res, dev) if res is not None else None
     Y = torch.empty((M, rc), dtype=torch.float32, device=dev)
-    say("sweep", seed, t, rc, k, M, layout, "fp32 x" if c["fp32x"] else "q8 x", "res" if c["res"] else "")
+    say("sweep", "raw" if raw else "", seed, t, rc, k, M, layout, "fp32 x" if c["fp32x"] else "q8 x", "res" if c["res"] else "")
     if M == 1 and c["fp32x"]:
         m27q.matvec(w, xd.view(-1), Y.view(-1), residual=None if resd is None else resd.view(-1))
     elif M == 1:
