@@ -344,7 +344,7 @@ def time_graph(torch, g, reps):
     return e0.elapsed_time(e1) / reps
 
 
-STREAM_SIZES_MB = (17.76, 23.65, 50.14, 73.22, 100.36, 200.0, 1000.0)
+STREAM_SIZES_MB = (4.456, 13.37, 17.76, 23.65, 50.14, 73.22, 100.36, 200.0, 1000.0)
 
 
 def stream_lib():
@@ -357,8 +357,8 @@ def stream_lib():
 
 
 def stream_read_peak(torch, dev, reps):
-    """GB/s of the plain streaming read at each size (the layer's product sizes,
-    200 MB and 1 GB), from HIP events over graph replays that rotate through
+    """GB/s of the plain streaming read at each size (the Q8_0 draft products'
+    sizes, the layer's product sizes, 200 MB and 1 GB), from HIP events over graph replays that rotate through
     >= 2 x the 256 MB Infinity Cache of distinct bytes (each read streams from
     HBM).  Every launch includes its dispatch, as the products' figures do."""
     L = stream_lib()
