@@ -233,7 +233,14 @@ __global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restr
         const int i = t + u * kTopkBlock;
         x0[u] = i < len ? v[base + i] : 0.f;
     }
-    if (t < nchunks) mk[t] = sc.maxkey[t];
+    // Slots past nchunks hold 0, which ranks below every key (no key is 0), so
+    // the rank loop runs over all kTopkMaxChunks slots, fully unrolled, in
+    // batches of 8 keys read while the previous batch is compared: with one
+    // wave per SIMD nothing else hides the LDS latency (top-64 of 248320:
+    // 11.1 us against 12.2 with a loop over nchunks, 11.6 fully unrolled
+    // without the batches).
+    static_assert(kTopkBlock == kTopkMaxChunks, "one thread per chunk-maximum slot");
+    mk[t] = t < nchunks ? sc.maxkey[t] : 0ull;
     if (t == 0) {
         bound = 0ull;  // fewer than k chunks: no bound
         local = 0u;
@@ -241,8 +248,25 @@ __global__ __launch_bounds__(kTopkBlock) void k_topk_filter(const float *__restr
     __syncthreads();
     if (t < nchunks) {
         const uint64_t me = mk[t];
+        constexpr int B = 8;
+        static_assert(kTopkMaxChunks % (2 * B) == 0, "whole pairs of batches");
+        uint64_t ka[B], kb[B];
         int rank = 0;
-        for (int j = 0; j < nchunks; ++j) rank += mk[j] > me;
+#pragma unroll
+        for (int i = 0; i < B; ++i) ka[i] = mk[i];
+#pragma unroll
+        for (int j0 = 0; j0 < kTopkMaxChunks; j0 += 2 * B) {
+#pragma unroll
+            for (int i = 0; i < B; ++i) kb[i] = mk[j0 + B + i];
+#pragma unroll
+            for (int i = 0; i < B; ++i) rank += ka[i] > me;
+            if (j0 + 2 * B < kTopkMaxChunks) {
+#pragma unroll
+                for (int i = 0; i < B; ++i) ka[i] = mk[j0 + 2 * B + i];
+            }
+#pragma unroll
+            for (int i = 0; i < B; ++i) rank += kb[i] > me;
+        }
         if (rank == k - 1) bound = me;  // the maxima are distinct keys: one thread
     }
     __syncthreads();
