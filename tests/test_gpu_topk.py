@@ -40,15 +40,19 @@ def test_topk_ties_zeros_nan_inf(m27q, ora, dev):
         oi, ov = ora.topk(v, k)
         assert np.array_equal(idx, oi)
         assert np.array_equal(val.view(np.uint32), ov.view(np.uint32))
-    # all equal: the first k indices, in order
+    # all equal: the first k indices, in order, each value with its own sign
     z = np.zeros(3000, np.float32)
     z[::2] = -0.0
-    idx, _ = run_topk(m27q, dev, z, 64)
+    idx, val = run_topk(m27q, dev, z, 64)
     assert list(idx) == list(range(64))
-    # NaN only beats padding: with n = k everything is returned, NaN last
+    assert np.array_equal(val.view(np.uint32), z[:64].view(np.uint32))
+    # NaN only beats padding: with n = k everything is returned, NaN last, each
+    # NaN with its own payload
     w = np.array([np.nan, 1.0, -np.inf, np.nan], np.float32)
-    idx, _ = run_topk(m27q, dev, w, 4)
+    w.view(np.uint32)[3] = 0xFFC00123
+    idx, val = run_topk(m27q, dev, w, 4)
     assert list(idx) == [1, 2, 0, 3]
+    assert np.array_equal(val.view(np.uint32), w[[1, 2, 0, 3]].view(np.uint32))
 
 
 @pytest.mark.parametrize("case,k", [("equal", 8), ("equal", 64), ("descending", 64), ("ascending", 33)])
