@@ -1,6 +1,6 @@
 """Seeded random shapes through every product entry point, against the
 integer-dot oracle: random type, layout, row count (ragged tiles), K (whole
-blocks, ragged Q8_0 units), token count M (the few-token GEMV, both MFMA
+blocks, ragged Q8_0 units), token count M up to the entry points' 64 (the few-token GEMV, both MFMA
 packings, the resident-activation kernel's 16-token launches and their
 remainders), fp32 or quantized activations, residual, multi-weight launches
 of mixed types and the SwiGLU epilogue.  The fixed cases elsewhere pin the
@@ -19,7 +19,7 @@ from test_oracle import random_blocks
 pytestmark = pytest.mark.gpu
 
 TYPES = ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"]
-MS = [1, 1, 1, 2, 2, 3, 4, 7, 8, 9, 16, 17, 24, 33]
+MS = [1, 1, 1, 2, 2, 3, 4, 7, 8, 9, 16, 17, 24, 33, 47, 64]
 
 
 def draw(seed):
