@@ -20,6 +20,7 @@ of untimed replays.
 value = weight bytes of the layer (GGUF, unpadded: 214,671,360 B) / step time.
 """
 import argparse
+import hashlib
 import json
 import os
 import re
@@ -40,6 +41,9 @@ LAYER = [  # name, type, rows, K
     ("down", "Q6_K", 5120, 17408),
 ]
 MALL_BYTES = 256 << 20
+# GGUF bytes of one 256-weight block of each type in the layer
+_BLOCK = {"Q4_K": 144, "Q6_K": 210}
+LAYER_BYTES = sum(_BLOCK[t] * rc * k // 256 for _, t, rc, k in LAYER)  # 214,671,360
 
 
 def load_pkg():
@@ -89,6 +93,10 @@ class Buffers:
     def __init__(self, m27q, dev):
         import torch
         self.x = torch.from_numpy(np.random.default_rng(1).standard_normal(5120).astype(np.float32)).to(dev)
+        # the attention layer's Wo input: the attention output (q stands in)
+        # gated by sigmoid(gate), quantized by m27q_quant_act_gated into qa
+        self.gate = torch.from_numpy(np.random.default_rng(2).standard_normal(6144).astype(np.float32)).to(dev)
+        self.qa = m27q.Act(1, 6144, dev)
         self.q = torch.empty(6144, dtype=torch.float32, device=dev)
         self.k = torch.empty(1024, dtype=torch.float32, device=dev)
         self.v = torch.empty(1024, dtype=torch.float32, device=dev)
@@ -110,6 +118,14 @@ STAGES = {
 }
 STAGE_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",),
                  "cfg1": ("gate",)}
+
+# The attention layer's form of the same products (exec:2451-2464): Wo's input
+# is the attention output gated by sigmoid(gate), quantized by a separate
+# launch (m27q_quant_act_gated, as k_quant_q8_1_fused_gate), then the product
+# on those codes with the residual (m27q_matvec_q8, as l_mv_q8_on).
+STAGES_ATTN = dict(STAGES)
+STAGES_ATTN["o"] = lambda m27q, L, B, s: (m27q.quant_act(B.q, B.qa, gate=B.gate, stream=s),
+                                          m27q.matvec_q8(L["o"], B.qa, B.h, residual=B.x, stream=s))
 
 # Config 4: the same products on M quantized activation rows (A[K] holds the M
 # rows of length K; Y[name] is [M][rows]).
@@ -147,18 +163,35 @@ def measured_traffic(kernel_label):
     return None
 
 
+def source_hash():
+    """sha256 (first 16 hex digits) of the library's sources: what a committed
+    profile is stamped with, so a figure read from it is used only while the
+    kernels it measured are the ones built here."""
+    h = hashlib.sha256()
+    pkg = os.path.join(ROOT, "mono-qwen27_amd")
+    files = sorted(os.path.join("csrc", f) for f in os.listdir(os.path.join(pkg, "csrc"))) + ["Makefile"]
+    for f in files:
+        h.update(f.encode())
+        h.update(open(os.path.join(pkg, f), "rb").read())
+    h.update(open(os.path.join(ROOT, "include", "m27q.h"), "rb").read())
+    return h.hexdigest()[:16]
+
+
 def profiled_kernel_us(kernel_label):
-    """Average kernel duration (us) of one product in the committed rocprofv3
-    --kernel-trace summary; None where that summary is absent.  HIP events over
-    graph replays see the same kernel plus the gap to the next dispatch."""
+    """Average kernel duration (us) of one product inside the layer graph, from
+    the committed rocprofv3 --kernel-trace summary, and whether that summary's
+    source stamp matches the sources here (None where it is absent)."""
     path = os.path.join(ROOT, "profiles", "gemv_decode_layer_kernel_trace.txt")
     if not os.path.exists(path):
-        return None
+        return None, False
+    us, stamp = None, None
     for line in open(path):
+        if line.startswith("sources:"):
+            stamp = line.split()[1]
         m = re.match(r"\s+" + re.escape(kernel_label) + r":.* avg\s+([0-9.]+) us", line)
-        if m:
-            return float(m.group(1))
-    return None
+        if m and us is None:
+            us = float(m.group(1))
+    return us, stamp == source_hash()
 
 
 def rand_weight(m27q, torch, dev, t, rc, k, layout=None):
@@ -208,14 +241,33 @@ def timed(torch, fn, ncopies, reps, warm=3, calls=32):
     return time_graph(torch, g, max(1, reps // rot)) / (rot * ncopies) * 1e3
 
 
-SECTIONS = ("cfg1", "cfg2", "cfg4", "cfg5", "decode")
+SECTIONS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "decode")
 
 
-def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
+def suite(m27q, torch, dev, layers, host, reps, sections=SECTIONS):
     """The other configurations of the path, each timed cold (rotated copies >= 2 x MALL)."""
     out = {}
     rng = np.random.default_rng(5)
     x5120 = torch.from_numpy(rng.standard_normal(5120).astype(np.float32)).to(dev)
+    if "cfg3" in sections:
+        # config 3 in the integration-faithful forms: (a) the attention layer,
+        # whose Wo takes the gated attention output through the separate
+        # gated quantizer; (b) the layer on weights in GGUF layout, uploaded
+        # verbatim as the reference's loader does (exec:1695-1716), no re-tiling
+        B = Buffers(m27q, dev)
+        us = timed(torch, lambda c, st: layer_pass(m27q, layers[c], B, st, STAGES_ATTN), len(layers), reps)
+        out["cfg3_attention_layer_gated_wo"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
+        log(f"attention layer (gated Wo): {us:.2f} us")
+        first = {}
+        for name, (t, rc, k, blocks) in host.items():
+            first[name] = m27q.Weight.upload(blocks.reshape(-1), t, k // 256, rc, m27q.GGUF, dev)
+        gl = [first] + [{n: m27q.Weight(w.data.clone(), w.type, w.rb, w.rc, w.layout) for n, w in first.items()}
+                        for _ in range(1, len(layers))]
+        torch.cuda.synchronize()
+        us = timed(torch, lambda c, st: layer_pass(m27q, gl[c], B, st), len(gl), reps)
+        out["cfg3_layer_gguf_layout"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
+        log(f"layer on GGUF-layout weights: {us:.2f} us")
+        del gl, first
     # config 1: Q4_K 17408 x 5120 alone, fp32 x
     if "cfg1" in sections:
         y = torch.empty(17408, dtype=torch.float32, device=dev)
@@ -247,8 +299,7 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
             for fn in STAGES_M.values():
                 fn(m27q, layers[c], acts, Ys, st)
         us = timed(torch, layer_m, len(layers), reps)
-        lb = sum(m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256 for _, t, rc, k in LAYER)
-        out[f"cfg4_layer_m{M}"] = {"us": round(us, 3), "GBps": round(lb / us / 1e3, 1)}
+        out[f"cfg4_layer_m{M}"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
         log(f"config 4 M={M}: {us:.2f} us")
     # config 5: LM head GEMV, exact top-64, 512-row gather
     if "cfg5" in sections or "decode" in sections:
@@ -280,7 +331,9 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
     # A decode step of linears, one graph with nothing on the host in between:
     # the embedding row of one token id (the 248320 x 5120 Q6_K table stands in
     # for token_embd), 64 layers of the layer's four products over the rotated
-    # cold copies, the LM head, the exact top-64 and the on-device sample.
+    # cold copies (every fourth layer, il % 4 == 3, is an attention layer whose
+    # Wo takes the gated quantizer's codes, exec:2451-2464), the LM head, the
+    # exact top-64 and the on-device sample.
     B = Buffers(m27q, dev)
     tok_id = torch.tensor([12345], dtype=torch.int32, device=dev)
     u = torch.full((1,), 0.3, dtype=torch.float32, device=dev)
@@ -289,7 +342,7 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
     def decode_step(c, st):
         m27q.embed_rows(lm, tok_id, B.x.view(1, 5120), stream=st)
         for li in range(64):
-            layer_pass(m27q, layers[li % len(layers)], B, st)
+            layer_pass(m27q, layers[li % len(layers)], B, st, STAGES_ATTN if li % 4 == 3 else STAGES)
         m27q.matvec(lm, B.out, logits, stream=st)
         m27q.topk(logits, k, idx, val, scratch, stream=st)
         m27q.sample(idx, val, k, 0.8, 0.05, 0.95, u, tok, stream=st)
@@ -299,8 +352,8 @@ def suite(m27q, torch, dev, layers, reps, sections=SECTIONS):
     return out
 
 
-def layer_pass(m27q, L, B, stream):
-    for fn in STAGES.values():
+def layer_pass(m27q, L, B, stream, stages=STAGES):
+    for fn in stages.values():
         fn(m27q, L, B, stream)
 
 
@@ -519,7 +572,7 @@ def main():
     if args.timeline:
         m27q.LIB_PATH = os.path.join(os.path.dirname(m27q.LIB_PATH), "libm27q_timeline.so")
     dev = torch.device("cuda:0")
-    layer_bytes = sum(m27q.BLOCK_BYTES[getattr(m27q, t)] * rc * k // 256 for _, t, rc, k in LAYER)
+    layer_bytes = LAYER_BYTES
     copies = args.copies or max(2, -(-2 * MALL_BYTES // layer_bytes) + 1)
     log(f"building {copies} layer copies ({layer_bytes * copies / 2**20:.0f} MiB)")
     layers, host = build_layers(m27q, ora, dev, copies)
@@ -529,68 +582,70 @@ def main():
         if bad:
             print(f"unknown sections {bad}; known: {SECTIONS}", file=sys.stderr)
             sys.exit(2)
-        print(json.dumps({"only": secs, "suite": suite(m27q, torch, dev, layers, max(1, args.steps // copies), secs)}))
+        print(json.dumps({"only": secs,
+                          "suite": suite(m27q, torch, dev, layers, host, max(1, args.steps // copies), secs)}))
         return
     B = Buffers(m27q, dev)
     if args.timeline:
         wave_timeline(m27q, torch, dev, layers, B)
         return
 
-    # A real decode step replays one graph for all its layers, so the layer's
-    # time is measured inside graphs of ROT rotations over the copies (32 layer
-    # passes): a graph launch boundary costs a few microseconds that a layer in
-    # the middle of a decode step does not pay.
-    ROT = 8
-    PG = ROT * copies
+    # A decode step replays one graph for all its layers, so the K timed layer
+    # passes replay one captured graph of exactly K passes (pass i on copy
+    # i mod copies, continuing after the W warmup passes; past MAXG passes, a
+    # graph of MAXG is replayed and a last one holds the remainder): the
+    # timed region has one graph launch boundary, as a decode step does.
+    MAXG = max(copies, 1024 // copies * copies)
 
-    def cold_pass(s, rot=1):
-        for _ in range(rot):
-            for L in layers:
-                layer_pass(m27q, L, B, s)
+    def passes(st, first, n):
+        for i in range(first, first + n):
+            layer_pass(m27q, layers[i % copies], B, st)
 
-    def warm_pass(s):
-        for _ in range(PG):
-            layer_pass(m27q, layers[0], B, s)
+    def pass_graphs(first, n):
+        """[(graph, replays)] running passes first .. first + n - 1."""
+        if n <= 0:
+            return []
+        q, r = divmod(n, MAXG)
+        out = []
+        if q:
+            out.append((capture(torch, lambda st: passes(st, first, MAXG)), q))
+        if r:
+            out.append((capture(torch, lambda st: passes(st, first + q * MAXG, r)), 1))
+        return out
+
+    def replay(gs):
+        for g, n in gs:
+            for _ in range(n):
+                g.replay()
 
     log("capturing graphs")
-    g_big = capture(torch, lambda st: cold_pass(st, ROT))
-    g_cold = capture(torch, cold_pass)
-    g_warm = capture(torch, warm_pass)
-    # one graph per copy, for the warm-up and step counts that are not whole rotations
-    g_one = [capture(torch, lambda st, L=L: layer_pass(m27q, L, B, st)) for L in layers]
-
-    def run_steps(n):
-        """Exactly n layer passes, continuing the rotation over the copies."""
-        q, r = divmod(n, PG)
-        for _ in range(q):
-            g_big.replay()
-        for _ in range(r // copies):
-            g_cold.replay()
-        for c in range(r % copies):
-            g_one[c].replay()
+    g_settle = capture(torch, lambda st: passes(st, 0, 8 * copies))
+    g_warmup = pass_graphs(0, args.warmup)
+    g_timed = pass_graphs(args.warmup, args.steps)
+    PG = 8 * copies
+    g_warm = capture(torch, lambda st: [layer_pass(m27q, layers[0], B, st) for _ in range(PG)])
 
     # The GPU's clocks settle first (untimed layer passes, SETTLE_MS_LAYER of
     # them), then the W warmup passes run, then the K timed ones.
-    settle(torch, g_big, SETTLE_MS_LAYER)
-    run_steps(args.warmup)
+    settle(torch, g_settle, SETTLE_MS_LAYER)
+    replay(g_warmup)
     torch.cuda.synchronize()
     log(f"timing {args.steps} layer passes")
     s0 = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(s0)
-    run_steps(args.steps)
+    replay(g_timed)
     e1.record(s0)
     e1.synchronize()
     ms_cold = e0.elapsed_time(e1) / args.steps
     reps = max(1, args.steps // copies)
-    greps = max(1, args.steps // PG)
-    ms_warm = time_graph(torch, g_warm, greps) / PG
-    # Spread: 10 batches of the big graph, each timed by one event pair with
-    # the batch's replays all enqueued (as the headline is), so the figures
-    # are comparable to it.
-    nb = max(1, greps // 4)
-    per = [time_graph(torch, g_big, nb) / PG * 1e3 for _ in range(10)]
+    ms_warm = time_graph(torch, g_warm, max(1, args.steps // PG)) / PG
+    # Spread: the timed graph (its first, or only, graph) replayed alone ten
+    # times, each replay timed by one event pair, as the headline is.
+    g0, _ = g_timed[0]
+    n0 = min(args.steps, MAXG)
+    per = [time_graph(torch, g0, 1) / n0 * 1e3 for _ in range(10)]
 
     # Each product on its own, over copies of its own weights that exceed the
     # Infinity Cache twice over (graphs of at least 32 launches): average launch
@@ -628,9 +683,8 @@ def main():
         del src, dst
 
     gbs = layer_bytes / (ms_cold * 1e-3) / 1e9
-    prof_us = profiled_kernel_us("gate_up")
-    ach_events = dom["GBps"]
-    ach = round(dom["bytes"] / (prof_us * 1e-6) / 1e9, 1) if prof_us else ach_events
+    prof_us, prof_current = profiled_kernel_us("gate_up")
+    ach = dom["GBps"]
     rec = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_cold, 5),
@@ -639,7 +693,7 @@ def main():
         "config": {"workload": "qwen27b_q4km_decode_layer_linears_m1",
                    "layer": {n: f"{t} {rc}x{k}" for n, t, rc, k in LAYER},
                    "weight_bytes": layer_bytes, "layout": "tiled", "activation": "int8 per-32, fp32 scale",
-                   "cold_copies": copies, "graph": True, "layer_passes_per_graph": PG,
+                   "cold_copies": copies, "graph": True, "layer_passes_per_graph": n0,
                    "untimed_settle_ms_before_warmup": SETTLE_MS_LAYER},
         "us_per_layer": round(ms_cold * 1e3, 2),
         "us_per_layer_batches_p10_median_p90": [round(float(np.percentile(per, q)), 2) for q in (10, 50, 90)],
@@ -653,19 +707,22 @@ def main():
                                                "fp32 x in, fp32 y out)",
                      "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up"),
-                     "achieved_source": ("rocprofv3 kernel average, profiles/gemv_decode_layer_kernel_trace.txt"
-                                         if prof_us else "HIP events (no committed kernel trace)"),
-                     "rocprof_kernel_avg_us": prof_us,
-                     "achieved_events": ach_events, "frac_events": round(ach_events / HBM_PEAK_GBS, 4),
+                     "achieved_source": "HIP events of this run: the product alone, graphs of >= 32 launches over "
+                                        "cold copies, on the replay stream (dispatch gap to the next launch included)",
                      "avg_launch_us_events": dom["us"],
+                     # the kernel inside the layer graph, from the committed
+                     # rocprofv3 trace; null when that trace was taken from
+                     # other sources than the ones built here
+                     "rocprof_kernel_avg_us_in_layer": prof_us if prof_current else None,
+                     "rocprof_source_stamp": source_hash(),
                      "measured_read_GBps_100MB_events": read_gbs.get("100.36MB"),
-                     "events_frac_of_measured_read": (round(ach_events / read_gbs["100.36MB"], 4)
-                                                      if read_gbs.get("100.36MB") else None),
+                     "frac_of_measured_read": (round(ach / read_gbs["100.36MB"], 4)
+                                               if read_gbs.get("100.36MB") else None),
                      "traffic_source": "profiles/gemv_decode_layer_hbm_traffic.txt",
                      "algorithmic_bytes": dom["bytes"]},
     }
     if not args.no_suite:
-        rec["suite"] = suite(m27q, torch, dev, layers, reps)
+        rec["suite"] = suite(m27q, torch, dev, layers, host, reps)
     if not args.no_cpu:
         log("cpu baseline")
         rec["cpu_baseline"] = cpu_baseline(ora, host)

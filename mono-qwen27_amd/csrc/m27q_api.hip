@@ -17,9 +17,6 @@ constexpr int kMaxK = 1 << 20;
 // Rows per weight: one-tile workgroups of up to 1024 threads keep every grid
 // below 2^32 work-items (the dispatch packet's limit).
 constexpr uint32_t kMaxRows = 1u << 24;
-#ifndef M27Q_BALANCE
-#define M27Q_BALANCE 1
-#endif
 constexpr int kMaxM = 64;
 constexpr int kMaxTopK = 64;
 
@@ -156,7 +153,7 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     // 6144 columns: 0.2 us slower), so fp32 input balances from 10240 columns.
     const long long tiles0 = tiles_of(ws[0].row_count);
     const int cus = cu_count();
-    const bool bal = M27Q_BALANCE && n == 1 && !swiglu && !yq && (!x || p.K >= 10240) && tiles0 > 2LL * cus &&
+    const bool bal = n == 1 && !swiglu && !yq && (!x || p.K >= 10240) && tiles0 > 2LL * cus &&
                      tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB) * cus;
     const int cfg = bal ? kCfgB
                         : pick_gemv_cfg(ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu, yq && !quant_after,
@@ -202,10 +199,7 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
 // (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).  Measured on the
 // Qwen-27B layer: 56 us against 63 at M = 2; from M = 3 on the MFMA kernel
 // with two row sets per tile is faster (63 against 75 us at M = 4).
-#ifndef M27Q_MT_MAXM
-#define M27Q_MT_MAXM 2
-#endif
-constexpr int kMtMaxM = M27Q_MT_MAXM;
+constexpr int kMtMaxM = 2;
 constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU
 
 m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,

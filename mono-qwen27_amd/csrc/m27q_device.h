@@ -11,8 +11,8 @@ namespace m27q {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
-// e^t, with t clamped to [-87, 87] (NaN is taken as -87), so that 2^n and
-// the result stay normal floats.  Cody-Waite range reduction (W. J. Cody and
+// e^t, with t clamped to [-87, 87], so that 2^n and the result stay normal
+// floats; a NaN t gives NaN back (so gated() and silu() propagate it).  Cody-Waite range reduction (W. J. Cody and
 // W. Waite, Software Manual for the Elementary Functions, 1980):
 // n = rint(t log2 e), r = t - n ln2 with ln2 split into a float and the
 // float of its remainder (the first FMA is exact), then the degree-7 Taylor
@@ -23,6 +23,7 @@ constexpr int kWave = 64;  // CDNA wavefront width
 // same bits; within 2 ulp of e^t.
 __device__ __forceinline__ float exp_cw(float t) {
 #pragma clang fp contract(off)
+    const float t0 = t;
     t = fminf(fmaxf(t, -87.0f), 87.0f);
     const float n = __builtin_rintf(t * 0x1.715476p+0f);
     float r = __builtin_fmaf(-n, 0x1.62e430p-1f, t);
@@ -35,7 +36,8 @@ __device__ __forceinline__ float exp_cw(float t) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return p * __int_as_float(((int)n + 127) << 23);
+    const float e = p * __int_as_float(((int)n + 127) << 23);
+    return __builtin_isnan(t0) ? t0 : e;
 }
 
 // x * sigmoid(g), the gated activation of k_quant_q8_1_fused_gate
@@ -114,7 +116,8 @@ __device__ __forceinline__ float sum8(float v) {
 // that is not finite: d == 0, or a subnormal d below 2^-128), code =
 // roundf(x * id) (one fp32 multiply, round half away from zero), clamped to
 // +-127.  A group whose id is 0 has all codes 0 (its values are below
-// 3.7e-37 in magnitude).  This is the rule of ggml's reference quantizer
+// 3.7e-37 in magnitude).  A NaN value stays out of amax (maxNum) and takes
+// code 0 (the float-to-int conversion of NaN); a group of NaNs has d = 0.  This is the rule of ggml's reference quantizer
 // quantize_row_q8_1_ref; the reference's GPU kernel (exec:84-107) writes
 // roundf(x / d) under fast-math, which compiles to the same multiply by an
 // approximate reciprocal.  Besides d, the two 16-value integer code sums are
@@ -168,7 +171,7 @@ __device__ __forceinline__ uint32_t pack_sums(int lo, int hi) {
 // One value per lane, one 32-lane half-wave per group.  Returns the code;
 // *d_out gets d and *s_out the packed sums (valid in every lane of the group).
 __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
-    float amax = fabsf(v);
+    float amax = fmaxf(fabsf(v), 0.0f);  // 0 for NaN
 #pragma unroll
     for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
     const float d = div127(amax);
@@ -197,7 +200,7 @@ __device__ __forceinline__ int quant32(float v, float *d_out, uint32_t *s_out) {
 // compiler's schedule of config 1's loop 0.4 us slower.
 __device__ __forceinline__ uint2 quant32x8(float4 a, float4 b, float *d_out, uint32_t *s_out) {
     float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                       fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+                       fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fmaxf(fabsf(b.w), 0.0f))));
     amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
     amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
     const float d = div127(amax);

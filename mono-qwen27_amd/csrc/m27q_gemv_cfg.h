@@ -59,8 +59,7 @@
 // GGUF-layout weights (the compatibility
 // path) follow the same rules: q/k/v 7.97 us and o 7.83 with them against 8.66
 // and 8.20 on (4,1) alone; gate/up and down pay for the row-major blocks
-// (30.6 and 21.6 us against 24.2 and 16.4 TILED).  Each shape can be
-// overridden at build time (-DM27Q_CFG_41=KS,TPW,WT ...) to sweep.
+// (30.6 and 21.6 us against 24.2 and 16.4 TILED).
 #pragma once
 
 namespace m27q {
@@ -73,39 +72,14 @@ struct GemvCfg {
     static_assert(NW >= 1 && NW <= 16, "a workgroup holds at most 16 wavefronts");
 };
 
-#ifndef M27Q_CFG_41
-#define M27Q_CFG_41 4, 1, 1, 1
-#endif
-#ifndef M27Q_CFG_81
-#define M27Q_CFG_81 8, 1, 1, 1
-#endif
-#ifndef M27Q_CFG_42
-#define M27Q_CFG_42 4, 2, 2, 1
-#endif
-#ifndef M27Q_CFG_84
-#define M27Q_CFG_84 8, 4, 2, 0
-#endif
-#ifndef M27Q_CFG_Q
-#define M27Q_CFG_Q 2, 4, 2, 1
-#endif
-#ifndef M27Q_CFG_161
-#define M27Q_CFG_161 16, 1, 1, 1
-#endif
-#ifndef M27Q_CFG_822
-#define M27Q_CFG_822 8, 2, 2, 0
-#endif
-#ifndef M27Q_CFG_B
-#define M27Q_CFG_B 4, 3, 1, 1
-#endif
-
-using Cfg41 = GemvCfg<M27Q_CFG_41>;
-using Cfg81 = GemvCfg<M27Q_CFG_81>;
-using Cfg42 = GemvCfg<M27Q_CFG_42>;
-using Cfg84 = GemvCfg<M27Q_CFG_84>;
-using CfgQ = GemvCfg<M27Q_CFG_Q>;
-using Cfg161 = GemvCfg<M27Q_CFG_161>;
-using Cfg822 = GemvCfg<M27Q_CFG_822>;
-using CfgB = GemvCfg<M27Q_CFG_B>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
+using Cfg41 = GemvCfg<4, 1, 1, 1>;
+using Cfg81 = GemvCfg<8, 1, 1, 1>;
+using Cfg42 = GemvCfg<4, 2, 2, 1>;
+using Cfg84 = GemvCfg<8, 4, 2, 0>;
+using CfgQ = GemvCfg<2, 4, 2, 1>;
+using Cfg161 = GemvCfg<16, 1, 1, 1>;
+using Cfg822 = GemvCfg<8, 2, 2, 0>;
+using CfgB = GemvCfg<4, 3, 1, 1>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
 static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 

@@ -203,24 +203,16 @@ static int pick_mt_cfg(long long rows, int upr) {
 // tiles of 24 units) 8.55-8.67 us against 8.95-9.2 with (8, 1, 1).  Down (68
 // units) measured 1.8 us slower that way: one 12-wave workgroup per CU hides
 // less latency than 2.5 of (8, 1, 1).
-#ifndef M27Q_MT_BALANCE
-#define M27Q_MT_BALANCE 1
-#endif
 int matmul_mt_balance(long long tiles, int upr, int cus) {
-    return M27Q_MT_BALANCE && upr < 40 && tiles > 2LL * cus && tiles <= (long long)CfgB::TPW * cus ? cus : 0;
+    return upr < 40 && tiles > 2LL * cus && tiles <= (long long)CfgB::TPW * cus ? cus : 0;
 }
 
 template <class T, int MT>
 static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
     if (p.bal_wgs > 0) return launch_mt_cfg<T, CfgB, MT>(p, s);
-#ifdef M27Q_MT_CFG
-    constexpr int forced = M27Q_MT_CFG;
-    const int cfg = forced;
-#else
     long long rows = 0;
     for (int i = 0; i < p.nmat; ++i) rows += p.rc[i];
     const int cfg = pick_mt_cfg(rows, p.upr);
-#endif
     switch (cfg) {
         case kCfg81: return launch_mt_cfg<T, Cfg81, MT>(p, s);
         case kCfg42: return launch_mt_cfg<T, Cfg42, MT>(p, s);

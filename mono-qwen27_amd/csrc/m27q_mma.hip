@@ -87,12 +87,8 @@ __device__ __forceinline__ v4u buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 }
 // Measured on the layer's products at M = 4 / 8 / 16 (cold weights): 61.2 /
 // 63.4 / 82.3 us per layer with non-temporal weight loads against 64.0 / 66.6
-// / 83.6 without; sc0 or sc1 added nothing either way (-DM27Q_MMA_NT=0 builds
-// the temporal form).
-#ifndef M27Q_MMA_NT
-#define M27Q_MMA_NT 1
-#endif
-constexpr int kWeightAux = M27Q_MMA_NT ? 2 : 0;
+// / 83.6 without; sc0 or sc1 added nothing either way.
+constexpr int kWeightAux = 2;
 __device__ __forceinline__ int s_lo(uint32_t s) { return (int)(int16_t)(s & 0xffffu); }
 __device__ __forceinline__ int s_hi(uint32_t s) { return (int)(int16_t)(s >> 16); }
 __device__ __forceinline__ float f4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
@@ -515,12 +511,9 @@ struct Stage {
 // 2 us faster than at 3), two-set launches 3; Q5_K and Q6_K one less (their
 // two-set launches have 160 row sets for 256 CUs at the model's shapes, so
 // the lower occupancy costs nothing).
-#ifndef M27Q_MM_WPE
-#define M27Q_MM_WPE 0
-#endif
 template <class T, int PK>
 constexpr int mm_waves_per_eu() {
-    return M27Q_MM_WPE ? M27Q_MM_WPE : (PK == 2 ? 3 : 4) - (T::kWide ? 1 : 0);
+    return (PK == 2 ? 3 : 4) - (T::kWide ? 1 : 0);
 }
 template <class T, int PK, int KS>
 __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmul_mfma(MatmulMultiParams p, int m0) {
@@ -738,10 +731,7 @@ struct XStage {
 
 // 16-byte activation chunks each thread has in flight while staging: 16
 // tokens x 6144 codes / 1024 threads in one round.
-#ifndef M27Q_XRES_BATCH
-#define M27Q_XRES_BATCH 6
-#endif
-constexpr int kXBatch = M27Q_XRES_BATCH;
+constexpr int kXBatch = 6;
 template <class T, int NWV>
 __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -948,16 +938,14 @@ static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
 }
 
 // The resident-activation kernel serves a launch of 16 tokens when every CU
-// gets at least M27Q_XRES_MIN_SETS_PER_CU row sets (the activation staging is
+// gets at least kXresMinSetsPerCu row sets (the activation staging is
 // paid once per workgroup) and its LDS fits.  16 waves per workgroup (every
 // type compiles within 128 registers, 4 waves per SIMD).  Measured on the
 // layer's gate/up (2176 sets): 32 us against 36 at M = 16, 32.5 against 33.5
 // at M = 12, where the layer's other launches ran about 0.3 us slower each
 // after it, so only full 16-token launches take it; q/k/v (2 sets per CU)
 // took 14 us against 9.5 with it.
-#ifndef M27Q_XRES_MIN_SETS_PER_CU
-#define M27Q_XRES_MIN_SETS_PER_CU 4
-#endif
+constexpr int kXresMinSetsPerCu = 4;
 template <class T>
 constexpr int xres_waves() {
     return 16;
@@ -972,7 +960,7 @@ static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *
     }
     p.wg_start[p.nmat] = S;
     const int cus = cu_count();
-    if (p.M - m0 < 16 || S < M27Q_XRES_MIN_SETS_PER_CU * cus) return false;
+    if (p.M - m0 < 16 || S < kXresMinSetsPerCu * cus) return false;
     const size_t lds = XStage<T>::bytes(p.upr, NWV);
     if (lds > lds_limit()) return false;
     // at most NWV sets per workgroup, so each wave's run covers at most two
@@ -990,22 +978,13 @@ static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *
 // 0.3 us faster; down (K = 17408) was 1.6 us slower so.  Two row sets per tile whenever at most 8 tokens are left
 // and the product has at least 128 sets of 32 rows (every product of the
 // layer): down at M = 8 takes 21.7 us against 28.8 with one-set tiles.
-#ifndef M27Q_MM_KS
-#define M27Q_MM_KS 0
-#endif
-#ifndef M27Q_MM_PK2_MIN_SETS
-#define M27Q_MM_PK2_MIN_SETS 128
-#endif
+constexpr int kPk2MinSets = 128;
 template <class T, int PK>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
     long long sets = 0;
     for (int i = 0; i < p.nmat; ++i) sets += (p.rc[i] + 16 * PK - 1) / (16 * PK);
-    const int ks = M27Q_MM_KS ? M27Q_MM_KS : (sets < 320 || (PK == 1 && p.K <= 6144)) ? 8 : 4;
-    switch (ks) {
-        case 2: return launch_mfma_t<T, PK, 2>(p, m0, s);
-        case 8: return launch_mfma_t<T, PK, 8>(p, m0, s);
-        default: return launch_mfma_t<T, PK, 4>(p, m0, s);
-    }
+    const int ks = (sets < 320 || (PK == 1 && p.K <= 6144)) ? 8 : 4;
+    return ks == 8 ? launch_mfma_t<T, PK, 8>(p, m0, s) : launch_mfma_t<T, PK, 4>(p, m0, s);
 }
 
 template <class T>
@@ -1014,7 +993,7 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
     for (int i = 0; i < p.nmat; ++i) sets32 += (p.rc[i] + 31) / 32;
     for (int m0 = 0; m0 < p.M;) {
         const int left = p.M - m0;
-        const bool pk2 = left <= 8 && sets32 >= M27Q_MM_PK2_MIN_SETS;
+        const bool pk2 = left <= 8 && sets32 >= kPk2MinSets;
         hipError_t e = hipSuccess;
         if (pk2)
             e = launch_mfma_pk<T, 2>(p, m0, s);

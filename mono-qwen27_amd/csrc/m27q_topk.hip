@@ -345,6 +345,8 @@ __global__ __launch_bounds__(kTopkSelBlock) void k_topk_select(const float *__re
     __shared__ SelectShared sh;
     __shared__ uint64_t best[kTopkMaxK];
     const int t = (int)threadIdx.x;
+    static_assert(kTopkSelBlock >= kTopkMaxChunks, "one thread per chunk count");
+    static_assert(kTopkMaxChunks == 4 * kWave, "the prefix below runs on one wave, 4 chunks per lane");
     if (t < kTopkMaxChunks) cnt[t] = t < nchunks ? sc.count[t] : 0u;
     __syncthreads();
     if (t < kWave) {  // exclusive prefix of the counts, 4 chunks per lane

@@ -450,7 +450,9 @@ static void quant_group32(const float *x, int8_t *q, float *d, uint32_t *s) {
     int lo = 0, hi = 0;
     for (int l = 0; l < 32; ++l) {
         const float t = x[l] * id;
-        const int v = clampi((int)roundf(t), -127, 127);
+        /* NaN (stays out of amax above) takes code 0, as the GPU's float-to-int
+         * conversion and the reference's __float2int_rn give it */
+        const int v = isnan(t) ? 0 : clampi((int)roundf(t), -127, 127);
         q[l] = (int8_t)v;
         if (l < 16) lo += v; else hi += v;
     }
@@ -462,7 +464,7 @@ void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s) 
     for (int64_t j = 0; j < k / 32; ++j) quant_group32(x + 32 * j, q + 32 * j, d + j, s + j);
 }
 
-/* e^t with t clamped to [-87, 87] (NaN taken as -87): the build's fixed exp,
+/* e^t with t clamped to [-87, 87] (NaN given back as NaN): the build's fixed exp,
  * so that host and device agree bit for bit.  Cody-Waite range reduction
  * (W. J. Cody and W. Waite, Software Manual for the Elementary Functions,
  * 1980): n = rint(t log2 e), r = t - n ln2 with ln2 = hi + lo in two floats
@@ -471,6 +473,7 @@ void ora_quant_act(const float *x, int64_t k, int8_t *q, float *d, uint32_t *s) 
  * the result are normal).  Pinned in tests/test_oracle.py against float64
  * exp (within 2 ulp over the whole range and at the clamp ends). */
 float ora_exp_cw(float t) {
+    if (isnan(t)) return t;
     t = fminf(fmaxf(t, -87.0f), 87.0f);
     const float n = rintf(t * 0x1.715476p+0f);
     float r = fmaf(-n, 0x1.62e430p-1f, t);

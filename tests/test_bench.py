@@ -45,3 +45,13 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=300, cwd=ROOT)
     assert r.returncode == 2
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_layer_bytes_and_source_stamp():
+    """LAYER_BYTES (behind value and the suite's layer figures) from the block
+    sizes; the source stamp that gates the profile-read kernel time is a
+    stable 16-hex-digit digest."""
+    import bench
+    assert bench.LAYER_BYTES == 214_671_360
+    h = bench.source_hash()
+    assert len(h) == 16 and int(h, 16) >= 0 and h == bench.source_hash()

@@ -18,6 +18,9 @@ def edge_rows(k):
     x[3] *= np.float32(1e30)                           # huge values
     x[4, ::2] = -x[4, ::2]
     x[5, :32] = -0.0
+    # NaN: out of the group's amax, code 0; a group of NaNs has d = 0
+    x[5, 64:72] = np.nan
+    x[5, 96:128] = np.nan
     # d = 1 again: values beside the ties and beside 0.5 (the largest float
     # below 0.5 must give 0, 0.5 itself 1) and subnormal inputs
     x[6, :32] = np.float32(127.0)
@@ -52,6 +55,8 @@ def gate_values(M, K, seed):
     g = (rng.standard_normal((M, K)) * 3).astype(np.float32)
     g[0, :8] = [0.0, -0.0, 87.0, -87.0, 90.0, -90.0, 1e4, -1e4]   # around and past the exp clamp
     g[0, 8:12] = [17.0, -17.0, 1e-30, -1e-30]
+    g[0, 12:14] = np.nan   # NaN gates give NaN values (code 0), not x
+    g[0, 32:64] = np.nan   # a group of them: d = 0
     return g
 
 

@@ -83,7 +83,8 @@ def test_q8_path_no_worse_than_q8K_cpu_path(m27q, ora, dev, type_name, rc, k):
     e_gpu = np.sqrt(np.mean((got - exact) ** 2))
     e_cpu = np.sqrt(np.mean((cpu - exact) ** 2))
     print(f"rms err gpu(per-32 int8)={e_gpu:.3e} cpu(q8_K/q8_0)={e_cpu:.3e} ratio={e_gpu / e_cpu:.3f}")
-    assert e_gpu <= e_cpu * 1.05
+    # north_star: no worse than the reference's own q8_K-activation path
+    assert e_gpu <= e_cpu, f"rms error ratio gpu/cpu = {e_gpu / e_cpu:.4f}"
 
 
 @pytest.mark.parametrize("layout", [0, 1])
@@ -318,6 +319,43 @@ def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k, layout):
     assert (got[rc:] == guard).all()
     m27q.matvec(w, xd, y0[:rc])
     assert np.array_equal(to_host(y0).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
+@pytest.mark.parametrize("rc,units", [(4098, 24), (5117, 2), (5120, 68)])
+def test_single_product_edges_every_type(m27q, ora, dev, type_name, rc, units):
+    """Single TILED products around the balanced-tiling rule, every integer-dot
+    type: 513 tiles with a last tile of 2 rows (24 units), 640 tiles with a last
+    tile of 5 rows and a single unit pair (fewer units than K slices: waves
+    with nothing to stream), and the 68-unit down shape (balanced tiling on
+    quantized input).  The quantized-input and the fp32-input products, each
+    with a residual, against the integer-dot oracle (in-kernel quantization
+    gives the same codes), the rows past row_count untouched."""
+    import torch
+    t = getattr(m27q, type_name)
+    k = units * (128 if type_name == "Q8_0" else 256)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = weights(ora, type_name, rc, k, 21)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal(k).astype(np.float32)
+    res = rng.standard_normal(rc).astype(np.float32)
+    xd, rd = to_dev(x, dev), to_dev(res, dev)
+    act = m27q.Act(1, k, dev)
+    m27q.quant_act(xd, act)
+    guard = np.float32(-7.25)
+    y0 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
+    y1 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
+    say("single product edges", type_name, rc, k)
+    m27q.matvec_q8(w, act, y1[:rc], residual=rd)
+    q, d, s = ora.quant_act(x)
+    want, nrm = ora.gemv_act(t, wb, rb, rc, q, d, s)
+    m27q.matvec(w, xd, y0[:rc], residual=rd)
+    for form, y in (("q8 x", y1), ("fp32 x", y0)):
+        got = to_host(y)
+        bad = np.abs(got[:rc].astype(np.float64) - (want + res)) > int_dot_tol(nrm) + 1e-6 * np.abs(res)
+        assert not bad.any(), (form, np.flatnonzero(bad)[:5], got[:rc][bad][:5], (want + res)[bad][:5])
+        assert (got[rc:] == guard).all(), form
 
 
 def test_fp32_input_multi_and_swiglu(m27q, ora, dev):

@@ -68,8 +68,7 @@ def test_matmul_vs_oracle(m27q, ora, dev, type_name, rc, k, M, layout):
     m27q.matmul_q8(w, act, Y, residual=to_dev(res, dev))
     got = to_host(Y).astype(np.float64) - res
     q, d, s = act_host(m27q, act)
-    rows = range(M) if M <= 8 else [0, 1, M // 2, M - 2, M - 1]
-    for m in rows:
+    for m in range(M):
         want, nrm = ora.gemv_act(t, wb, rb, rc, q[m], d[m], s[m])
         assert (np.abs(got[m] - want) <= int_dot_tol(nrm) + 1e-6 * np.abs(res[m])).all(), m
 
@@ -115,6 +114,6 @@ def test_matmul_multi_resident_vs_oracle(m27q, ora, dev, M, rows):
     q, d, s = act_host(m27q, act)
     for wb, rc, Y in zip(wbs, shapes, Ys):
         got = to_host(Y).astype(np.float64)
-        for m in sorted({0, M // 2, M - 1}):
+        for m in range(M):
             want, nrm = ora.gemv_act(m27q.Q4_K, wb, 4, rc, q[m], d[m], s[m])
             assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)

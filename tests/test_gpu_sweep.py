@@ -1,9 +1,12 @@
 """Seeded random shapes through every product entry point, against the
 integer-dot oracle: random type, layout, row count (ragged tiles), K (whole
 blocks, ragged Q8_0 units), token count M up to the entry points' 64 (the few-token GEMV, both MFMA
-packings, the resident-activation kernel's 16-token launches and their
-remainders), fp32 or quantized activations, residual, multi-weight launches
-of mixed types and the SwiGLU epilogue.  The fixed cases elsewhere pin the
+packings, 16-token launches and their remainders), fp32 or quantized
+activations, residual, multi-weight launches of mixed types and the SwiGLU
+epilogue.  Those draw at most 3000 rows, too few for the resident-activation
+kernel (16-token launches over >= 4 row sets of 16 per CU: 16369 rows on 256
+CUs); a third set of seeds draws 16400-20000 rows and 16-40 tokens for it,
+every token row checked.  The fixed cases elsewhere pin the
 benched shapes and the edges the kernels were written for; these cover the
 combinations between them (any layout, except multi-weight launches of
 several tokens, which take TILED weights).  A second set of seeds draws the
@@ -50,6 +53,39 @@ def test_random_product_vs_oracle(m27q, ora, dev, seed):
 @pytest.mark.parametrize("seed", range(5000, 5032))
 def test_random_bytes_vs_oracle(m27q, ora, dev, seed):
     run_case(m27q, ora, dev, seed, raw=True)
+
+
+@pytest.mark.parametrize("seed", range(9000, 9006))
+def test_random_resident_vs_oracle(m27q, ora, dev, seed):
+    """Random type, 16400-20000 rows (ragged last set), small K, 16-40 tokens
+    (resident 16-token launches, then the remainder on the per-unit kernel),
+    one or two weights of one K; every token row against the oracle."""
+    import torch
+    r = np.random.default_rng(3000 + seed)
+    t = TYPES[r.integers(len(TYPES))]
+    k = int(128 * r.integers(2, 9)) if t == "Q8_0" else int(256 * r.integers(1, 5))
+    M = int(r.integers(16, 41))
+    n = int(r.integers(1, 3))
+    mats = []
+    for i in range(n):
+        rc = int(r.integers(16400, 20001))
+        tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, m27q.TILED, seed + 100 * i)
+        mats.append((tid, wb, rb, w, rc))
+    X = r.standard_normal((M, k)).astype(np.float32)
+    act = m27q.Act(M, k, dev)
+    m27q.quant_act(to_dev(X, dev), act)
+    q, d, s = act_host(m27q, act)
+    Ys = [torch.empty((M, m[4]), dtype=torch.float32, device=dev) for m in mats]
+    say("sweep resident", seed, t, [m[4] for m in mats], k, M)
+    if n == 1:
+        m27q.matmul_q8(mats[0][3], act, Ys[0])
+    else:
+        m27q.matmul_q8_multi([m[3] for m in mats], act, Ys)
+    for (tid, wb, rb, _, rc), Y in zip(mats, Ys):
+        got = to_host(Y).astype(np.float64)
+        for m in range(M):
+            want, nrm = ora.gemv_act(tid, wb, rb, rc, q[m], d[m], s[m])
+            assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (seed, rc, m)
 
 
 def run_case(m27q, ora, dev, seed, raw):

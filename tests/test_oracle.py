@@ -279,6 +279,23 @@ def test_quant_act_matches_numpy_restatement(ora):
     assert (q[0, :32] == 0).all() and (q[1, 32:64] == 0).all()
 
 
+def test_quant_act_nan_rule(ora):
+    """NaN values stay out of the group's amax and take code 0; a group of
+    NaNs has d = 0 and all codes 0 (the GPU's maxNum and float-to-int rules)."""
+    x = RNG.standard_normal(96).astype(np.float32)
+    x[3], x[17] = np.nan, -np.nan
+    x[64:96] = np.nan
+    q, d, s = ora.quant_act(x)
+    fin = x[:32][~np.isnan(x[:32])]
+    assert d[0] == np.float32(np.abs(fin).max() / np.float32(127))
+    assert q[3] == 0 and q[17] == 0 and (q[64:96] == 0).all() and d[2] == 0 and s[2] == 0
+    # the finite values of the group quantize as they would with the NaNs at 0
+    x0 = x.copy()
+    x0[[3, 17]] = 0.0
+    q0, d0, _ = ora.quant_act(x0[:32])
+    assert np.array_equal(q[:32], q0) and d[0] == d0[0]
+
+
 def test_quant_act_rounds_half_away_from_zero(ora):
     x = np.zeros(32, np.float32)
     x[0] = 127.0  # d = 1 exactly
@@ -364,9 +381,13 @@ def test_exp_cw_within_2_ulp(ora):
     assert np.all(np.isfinite(got)) and np.all(got > 0)
     assert _ulps(got, np.exp(t.astype(np.float64))).max() <= 2.0
     assert ora.exp_cw(np.float32([0.0, -0.0]))[0] == 1.0
-    ends = ora.exp_cw(np.float32([-1e4, -88.0, np.nan, -np.inf, 1e4, 88.0, np.inf]))
+    ends = ora.exp_cw(np.float32([-1e4, -88.0, -np.inf, 1e4, 88.0, np.inf]))
     e_lo, e_hi = ora.exp_cw(np.float32([-87.0, 87.0]))
-    assert np.array_equal(ends, np.float32([e_lo] * 4 + [e_hi] * 3))
+    assert np.array_equal(ends, np.float32([e_lo] * 3 + [e_hi] * 3))
+    # NaN comes back as NaN, so a NaN gate propagates through gated() instead
+    # of letting x through
+    assert np.isnan(ora.exp_cw(np.float32([np.nan]))).all()
+    assert np.isnan(ora.gated(np.float32([1.5, -2.0]), np.float32([np.nan, np.nan]))).all()
     # monotone over a fine sorted sweep (an off coefficient would show as a step)
     s = np.sort(t)
     assert np.all(np.diff(ora.exp_cw(s).astype(np.float64)) >= 0)
