@@ -84,6 +84,34 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
     }
 }
 
+// Raw buffer loads: a scalar base (the descriptor) and scalar offset, a 32-bit
+// per-lane offset, no per-lane address arithmetic.  The record count is the
+// buffer's size, so a read past it returns zeros and touches no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// AUX is the cache policy: 2 marks the load non-temporal (buffer_load ... nt).
+template <int AUX = 0>
+__device__ __forceinline__ uint4 bld_u128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v v = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <int AUX = 0>
+__device__ __forceinline__ uint2 bld_u64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+    const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, AUX));
+    return make_uint2(v.x, v.y);
+}
+template <int AUX = 0>
+__device__ __forceinline__ uint32_t bld_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, AUX);
+}
+template <int AUX = 0>
+__device__ __forceinline__ uint32_t bld_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, AUX);
+}
+
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask, int width = kWave) {
     return __shfl_xor(v, mask, width);

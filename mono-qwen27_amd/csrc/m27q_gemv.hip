@@ -44,8 +44,8 @@
 
 namespace m27q {
 
-// Activation staging into LDS: codes[Kp] | d[Kp/32] | aux[Kp/32] (zero
-// padded from K to Kp).  stage_load() loads one batch into registers (the
+// Activation staging into LDS: codes[Kp] | d[Kp/32] | aux[Kp/32 * T::kAuxWords]
+// (zero padded from K to Kp).  stage_load() loads one batch into registers (the
 // first before the first weight loads), stage_store() converts and stores it.
 constexpr int kStageSlots = 4;  // per thread: 4 x 32 B of fp32 values, or 4 x 16 B of codes
 
@@ -103,7 +103,7 @@ __device__ __forceinline__ void stage_store(const StageRegs<XF32> &r, uint8_t *s
                 ((uint2 *)xc)[j] = quant32x8(r.v[b][0], r.v[b][1], &d, &s);
                 if ((j & 3) == 0) {
                     xd[j / 4] = d;
-                    xs[j / 4] = T::stage_aux(d, s);
+                    T::put_aux(xs, j / 4, d, s);
                 }
             }
         }
@@ -114,7 +114,7 @@ __device__ __forceinline__ void stage_store(const StageRegs<XF32> &r, uint8_t *s
             if (j < Kp / 16) ((uint4 *)xc)[j] = r.v[b];
             if (j < Kp / 32) {
                 xd[j] = r.d[b];
-                xs[j] = T::stage_aux(r.d[b], r.s[b]);
+                T::put_aux(xs, j, r.d[b], r.s[b]);
             }
         }
     }
@@ -233,7 +233,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     const uint8_t *W[NM];
     W[0] = p.W[m];
     if constexpr (SWIGLU) W[NM - 1] = p.W[1];
-    const UnitStream<T, LAYOUT, NM, WT, C::NT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, p.rb, p.upr, lane);
+    // buffer loads for the Q6_K stream only (see UnitStream)
+    const UnitStream<T, LAYOUT, NM, WT, C::NT, T::kType == kQ6_K> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc,
+                                                                      p.rb, p.upr, lane);
     typename T::Frag fa[NM][WT], fb[NM][WT];
     ws.load(fa, min(ub, p.upr - 1));
 
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
         stage_store<T, XF32>(sr, smem, Kp, j0, nth);
     }
     const ActLds act{(const int8_t *)smem, (const float *)(smem + Kp), (const uint32_t *)(smem + Kp + Kp / 8)};
-    float *red = (float *)(smem + Kp + Kp / 4);  // [NM][KS][NR]
+    float *red = (float *)(smem + Kp + Kp / 8 * (1 + T::kAuxWords));  // [NM][KS][NR]
     __syncthreads();
 #ifdef M27Q_WAVE_TIMELINE
     const unsigned long long tl_staged = __builtin_amdgcn_s_memrealtime();
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(256) void k_gemv_dense(GemvParams p) {
 template <class T, class C, bool SWIGLU>
 size_t gemv_q8_lds(int upr) {
     const size_t Kp = (size_t)upr * T::kUnitElems;
-    return Kp + Kp / 4 + (size_t)(SWIGLU ? 2 : 1) * C::KS * C::TPW * kTileRows * sizeof(float);
+    return Kp + Kp / 8 * (1 + T::kAuxWords) + (size_t)(SWIGLU ? 2 : 1) * C::KS * C::TPW * kTileRows * sizeof(float);
 }
 
 template <class T, int LAYOUT, class C, bool SWIGLU, bool XF32>

@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     ws.load(fa, min(ub, p.upr - 1));
 
     // Activations of tokens m0 .. m0 + MT: codes [MT][Kp] | d [MT][Kp/32] |
-    // aux [MT][Kp/32], zero past K and past M.  Loads go out 4 per thread
+    // aux [MT][Kp/32 * T::kAuxWords], zero past K and past M.  Loads go out 4 per thread
     // before their stores.
     const int Kp = p.upr * T::kUnitElems, gp = Kp / 32, ng = p.K / 32;
     const int nq = Kp / 16;
@@ -98,11 +98,11 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
             const int j = j0 + b * nth;
             if (j < MT * gp) {
                 xd[j] = d[b];
-                xs[j] = T::stage_aux(d[b], s[b]);
+                T::put_aux(xs, j, d[b], s[b]);
             }
         }
     }
-    float *red = (float *)(xs + MT * gp);  // [MT][KS][NR]
+    float *red = (float *)(xs + MT * gp * T::kAuxWords);  // [MT][KS][NR]
     __syncthreads();
 
     float acc[MT][WT];
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     auto compute = [&](const typename T::Frag (&f)[1][WT], int u) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const ActLds act{xc + (size_t)mt * Kp, xd + mt * gp, xs + mt * gp};
+            const ActLds act{xc + (size_t)mt * Kp, xd + mt * gp, xs + mt * gp * T::kAuxWords};
             const typename T::AFrag a = T::load_act(act, u, ws.L);
 #pragma unroll
             for (int t = 0; t < WT; ++t) acc[mt][t] += T::dot(f[0][t], a, ws.L);
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
 template <class T, class C, int MT>
 static size_t mt_lds(int upr) {
     const size_t Kp = (size_t)upr * T::kUnitElems;
-    return MT * (Kp + Kp / 4) + (size_t)MT * C::KS * C::TPW * kTileRows * sizeof(float);
+    return MT * (Kp + Kp / 8 * (1 + T::kAuxWords)) + (size_t)MT * C::KS * C::TPW * kTileRows * sizeof(float);
 }
 
 template <class T, class C, int MT>

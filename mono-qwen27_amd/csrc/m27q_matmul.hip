@@ -19,7 +19,7 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
     constexpr int CK = kChunkUnits * T::kUnitElems;  // activation values per chunk
     int8_t *xc = (int8_t *)smem;                    // [MT][CK]
     float *xd = (float *)(smem + MT * CK);           // [MT][CK/32]
-    uint32_t *xs = (uint32_t *)(xd + MT * CK / 32);  // [MT][CK/32]
+    uint32_t *xs = (uint32_t *)(xd + MT * CK / 32);  // [MT][CK/32 * T::kAuxWords]
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane >> 3, c = lane & 7;
     const int rc = p.rc;
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
                 s = p.xs[(size_t)(m0 + m) * (p.K / 32) + gpos];
             }
             xd[j] = d;
-            xs[j] = T::stage_aux(d, s);
+            T::put_aux(xs, j, d, s);
         }
         __syncthreads();
         if (tile < ntiles) {
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
                 if (u0 + k < p.upr) {
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        const ActLds a{xc + m * CK, xd + m * (CK / 32), xs + m * (CK / 32)};
+                        const ActLds a{xc + m * CK, xd + m * (CK / 32), xs + m * (CK / 32) * T::kAuxWords};
                         acc[m] += T::dot(f[k], a, k, L);
                     }
                 }
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
 template <class T, int LAYOUT, int MT>
 static hipError_t launch_mt(const MatmulParams &p, int m0, hipStream_t s) {
     constexpr int CK = kChunkUnits * T::kUnitElems;
-    const size_t lds = (size_t)MT * CK + (size_t)MT * CK / 32 * 8;
+    const size_t lds = (size_t)MT * CK + (size_t)MT * CK / 32 * 4 * (1 + T::kAuxWords);
     const int grid = (((p.rc + kTileRows - 1) / kTileRows) + kWavesPerWG - 1) / kWavesPerWG;
     hipLaunchKernelGGL((k_matmul_q8<T, LAYOUT, MT>), dim3(grid), dim3(256), lds, s, p, m0);
     return hipGetLastError();

@@ -73,14 +73,9 @@ __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; }
-// Raw buffer loads: a scalar base (the descriptor) and scalar offset, a 32-bit
-// per-lane offset, no per-lane address arithmetic.  The record count is the
-// buffer's size, so a read past it returns zeros and touches no memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-// AUX is the cache policy: 2 marks the load non-temporal (buffer_load ... nt),
-// the policy of the weight streams, which are read once per product.
+// Raw buffer loads (buf_rsrc, m27q_device.h).  AUX is the cache policy: 2
+// marks the load non-temporal (buffer_load ... nt), the policy of the weight
+// streams, which are read once per product.
 template <int AUX = 0>
 __device__ __forceinline__ v4u buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));

@@ -10,7 +10,7 @@
 // Activations are staged in LDS by the calling kernel:
 //   int8  xc[Kp]       codes (Kp = K padded to whole units, pad = 0)
 //   float xd[Kp/32]    per-32 scale
-//   u32   xs[Kp/32]    per-type auxiliary word (see stage_aux)
+//   u32   xs[Kp/32 * T::kAuxWords]  per-type auxiliary words (T::put_aux)
 // and, for the fp32-activation kernels:
 //   float xf[Kp]       values
 //   float x16[Kp/16]   per-16 sums of the values
@@ -94,6 +94,11 @@ struct Q4K {
         const uint8_t *blk = row + (size_t)u * kQ4KBytes;
         return {ld_u128<NT>(blk + kQ4KHdr + 16 * c), ld_u128<NT>(blk)};
     }
+    // The same planes through a buffer descriptor of the tile; soff = the unit's offset.
+    template <int AUX>
+    __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &) {
+        return {bld_u128<AUX>(r, 128 + 128 * i + 16 * c, soff), bld_u128<AUX>(r, 16 * i, soff)};
+    }
 
     // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c.
     __device__ static uint32_t scale_pair(const uint4 &h, const Lane &L) {
@@ -105,10 +110,12 @@ struct Q4K {
         return (int)(((Y >> L.mx) & L.mm) | ((h.z >> L.my) & L.mh));
     }
 
-    // LDS aux word: d * (sum of the 32 codes), the scale of the block-min term.
-    __device__ static uint32_t stage_aux(float d, uint32_t s) {
+    // LDS aux word of group g: d * (sum of the 32 codes), the scale of the
+    // block-min term.
+    static constexpr int kAuxWords = 1;
+    __device__ static void put_aux(uint32_t *xs, int g, float d, uint32_t s) {
         const int S = (int)(int16_t)(s & 0xffffu) + (int)(int16_t)(s >> 16);
-        return __float_as_uint(d * (float)S);
+        xs[g] = __float_as_uint(d * (float)S);
     }
 
     __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
@@ -200,6 +207,11 @@ struct Q5K : Q4K {
         const uint8_t *blk = row + (size_t)u * kQ5KBytes;
         return {ld_u128<NT>(blk + kQ5KQs + 16 * c), ld_u128<NT>(blk + kQ5KQh + 16 * (c & 1)), ld_u128<NT>(blk)};
     }
+    template <int AUX>
+    __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &) {
+        return {bld_u128<AUX>(r, 128 + 128 * i + 16 * c, soff), bld_u128<AUX>(r, kQ5KTQh + 32 * i + 16 * (c & 1), soff),
+                bld_u128<AUX>(r, 16 * i, soff)};
+    }
 
     // 5-bit codes of one dword: the nibbles plus bit 2g (low) / 2g + 1 (high)
     // of each qh byte, moved to bit 4.  Shifted right first: a left shift of the
@@ -267,8 +279,8 @@ struct Q6K {
     };
 
     struct Lane {
-        int hh, cc, qh_off, aoff, jlo, shl_lo, shr_hi;
-        bool hsel;
+        int hh, cc, qh_off, aoff, jlo, shl_lo, shr_hi, hsel;
+        uint32_t scsel;  // v_perm_b32: byte cc of sc.x, byte cc of sc.y
         __device__ explicit Lane(int c) {
             hh = c >> 2;
             cc = c & 3;
@@ -278,7 +290,8 @@ struct Q6K {
             jlo = 4 * hh + r;
             shl_lo = 4 - 2 * r;
             shr_hi = 2 * (r + 2) - 4;
-            hsel = (cc & 1) != 0;
+            hsel = cc & 1;
+            scsel = 0x0c0c0000u | ((uint32_t)(cc + 4) << 8) | (uint32_t)cc;
         }
     };
 
@@ -289,6 +302,16 @@ struct Q6K {
         f.qh = ld_u128<NT>(unit + kQ6KTQh + 64 * i + L.qh_off);
         f.sc = *(const uint2 *)(unit + kQ6KTSc + 16 * i + 8 * L.hh);
         f.d = *(const uint32_t *)(unit + kQ6KTD + 4 * (i >> 1));  // the d pair of rows i & ~1, i | 1
+        f.dsh = 16 * (i & 1);
+        return f;
+    }
+    template <int AUX>
+    __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &L) {
+        Frag f;
+        f.ql = bld_u128<AUX>(r, kQ6KTQl + 128 * i + 16 * c, soff);
+        f.qh = bld_u128<AUX>(r, kQ6KTQh + 64 * i + L.qh_off, soff);
+        f.sc = bld_u64(r, kQ6KTSc + 16 * i + 8 * L.hh, soff);
+        f.d = bld_u32(r, kQ6KTD + 4 * (i >> 1), soff);  // the d pair of rows i & ~1, i | 1
         f.dsh = 16 * (i & 1);
         return f;
     }
@@ -304,7 +327,14 @@ struct Q6K {
         return f;
     }
 
-    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }
+    // LDS aux words of group g: -32 x the code sums of its two 16-value
+    // halves.  The weight codes are q + 32, so the dot sums start from these
+    // and the offset is removed exactly.
+    static constexpr int kAuxWords = 2;
+    __device__ static void put_aux(uint32_t *xs, int g, float, uint32_t s) {
+        xs[2 * g] = (uint32_t)(-32 * (int)(int16_t)(s & 0xffffu));
+        xs[2 * g + 1] = (uint32_t)(-32 * (int)(int16_t)(s >> 16));
+    }
 
     __device__ static void codes(const Frag &f, const Lane &L, uint32_t lo6[4], uint32_t hi6[4]) {
         const uint32_t qlw[4] = {f.ql.x, f.ql.y, f.ql.z, f.ql.w};
@@ -316,13 +346,8 @@ struct Q6K {
         }
     }
 
-    __device__ static int s16(uint32_t s, bool hi) {
-        return hi ? (int)(int16_t)(s >> 16) : (int)(int16_t)(s & 0xffffu);
-    }
-
     // Activation fragment of one unit for lane c: 2 x 16 codes, their scales,
-    // and 32 x (code sums): the weight codes are q + 32, so the offset is
-    // removed exactly with these integer sums.
+    // and -32 x (code sums) of the two 16-value halves.
     struct AFrag {
         int4 lo, hi;
         float dlo, dhi;
@@ -336,8 +361,8 @@ struct Q6K {
         const int jl = 8 * u + L.jlo;
         r.dlo = a.xd[jl];
         r.dhi = a.xd[jl + 2];
-        r.olo = 32 * s16(a.xs[jl], L.hsel);
-        r.ohi = 32 * s16(a.xs[jl + 2], L.hsel);
+        r.olo = (int)a.xs[2 * jl + L.hsel];
+        r.ohi = (int)a.xs[2 * jl + 4 + L.hsel];
         return r;
     }
 
@@ -345,18 +370,17 @@ struct Q6K {
     __device__ static float dot(const Frag &f, const AFrag &a, const Lane &L) {
         uint32_t lo6[4], hi6[4];
         codes(f, L, lo6, hi6);
-        int slo = dot4((int)lo6[0], a.lo.x, 0);
+        int slo = dot4((int)lo6[0], a.lo.x, a.olo);
         slo = dot4((int)lo6[1], a.lo.y, slo);
         slo = dot4((int)lo6[2], a.lo.z, slo);
         slo = dot4((int)lo6[3], a.lo.w, slo);
-        int shi = dot4((int)hi6[0], a.hi.x, 0);
+        int shi = dot4((int)hi6[0], a.hi.x, a.ohi);
         shi = dot4((int)hi6[1], a.hi.y, shi);
         shi = dot4((int)hi6[2], a.hi.z, shi);
         shi = dot4((int)hi6[3], a.hi.w, shi);
-        slo -= a.olo;
-        shi -= a.ohi;
-        const int sclo = (int)(int8_t)(f.sc.x >> (8 * L.cc));
-        const int schi = (int)(int8_t)(f.sc.y >> (8 * L.cc));
+        const uint32_t sp = __builtin_amdgcn_perm(f.sc.y, f.sc.x, L.scsel);
+        const int sclo = (int)(int8_t)sp;
+        const int schi = (int)(int8_t)(sp >> 8);
         // |sums| <= 32 * 127 * 16 < 2^23 and |scales| <= 128: exact 24-bit products.
         const float t = fmaf(a.dhi, (float)__mul24(shi, schi), a.dlo * (float)__mul24(slo, sclo));
         return f16_bits_to_f32(f.d >> f.dsh) * t;
@@ -416,13 +440,18 @@ struct IQ4XS {
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
         return {ld_u128<NT>(unit + 128 * i + 16 * c), *(const uint2 *)(unit + kIQ4XSTHdr + 8 * i)};
     }
+    template <int AUX>
+    __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &) {
+        return {bld_u128<AUX>(r, 128 * i + 16 * c, soff), bld_u64(r, kIQ4XSTHdr + 8 * i, soff)};
+    }
     template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
         const uint8_t *blk = row + (size_t)u * kIQ4XSBytes;
         const uint2 a = *(const uint2 *)(blk + kIQ4XSQs + 16 * c), b = *(const uint2 *)(blk + kIQ4XSQs + 16 * c + 8);
         return {make_uint4(a.x, a.y, b.x, b.y), *(const uint2 *)blk};
     }
-    __device__ static uint32_t stage_aux(float, uint32_t s) { return s; }
+    static constexpr int kAuxWords = 0;  // codes and scales only
+    __device__ static void put_aux(uint32_t *, int, float, uint32_t) {}
 
     __device__ static AFrag load_act(const ActLds &a, int u, const Lane &L) {
         AFrag r;
@@ -491,6 +520,10 @@ struct Q80 {
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int /*c*/, const Lane &L) {
         return {ld_u128<NT>(unit + 128 * i + 32 * L.k + 16 * L.hf), *(const uint16_t *)(unit + kQ80TD + 8 * i + 2 * L.k)};
     }
+    template <int AUX>
+    __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int /*c*/, const Lane &L) {
+        return {bld_u128<AUX>(r, 128 * i + 32 * L.k + 16 * L.hf, soff), bld_u16(r, kQ80TD + 8 * i + 2 * L.k, soff)};
+    }
     template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int rb, int /*c*/, const Lane &L) {
         const int bi = 4 * u + L.k;
@@ -499,7 +532,8 @@ struct Q80 {
         return {ld_u128_a2(blk + 2 + 16 * L.hf), *(const uint16_t *)blk};
     }
 
-    __device__ static uint32_t stage_aux(float, uint32_t) { return 0u; }
+    static constexpr int kAuxWords = 0;  // codes and scales only
+    __device__ static void put_aux(uint32_t *, int, float, uint32_t) {}
 
     struct AFrag {
         int4 x;
@@ -544,8 +578,17 @@ struct Q80 {
 // includes m27q.h for the layout tags).  NT selects non-temporal 16-byte loads
 // (ld_u128<true>); the GGUF blocks that are only 2- or 8-byte aligned (Q6_K,
 // Q8_0, IQ4_XS) are read in smaller pieces and keep the default policy.
-template <class T, int LAYOUT, int NM, int TPW, bool NT = false>
+// With BUF, TILED weights are read through one buffer descriptor per tile
+// (its base and byte count in scalar registers): the plane offsets of the
+// lane are one loop-invariant register and the unit's offset a scalar, so a
+// load costs no vector address arithmetic (with 64-bit per-lane addresses it
+// cost 3-7 vector instructions per unit).  Measured per kernel (its callers
+// choose): down 0.2 us and the few-token layer 1 us faster with them, the
+// multi-tile Q4_K shapes (config 1, o) 0.2-0.5 us slower.
+template <class T, int LAYOUT, int NM, int TPW, bool NT = false, bool BUF = true>
 struct UnitStream {
+    static constexpr bool kTiled = LAYOUT == M27Q_LAYOUT_TILED, kBuf = kTiled && BUF;
+    __amdgpu_buffer_rsrc_t rs[kBuf ? NM : 1][kBuf ? TPW : 1];  // TILED with BUF: one tile each
     const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
     int i, c, rb;
     typename T::Lane L;
@@ -557,8 +600,10 @@ struct UnitStream {
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
                 const int tile = min(tile0 + t, ntiles - 1);  // past the end: reread the last tile
-                if constexpr (LAYOUT == M27Q_LAYOUT_TILED) {
-                    base[m][t] = W[m] + (size_t)tile * upr * T::kUnitBytes;
+                if constexpr (kTiled) {
+                    const uint32_t tb = (uint32_t)upr * (uint32_t)T::kUnitBytes;
+                    base[m][t] = W[m] + (size_t)tile * tb;
+                    if constexpr (kBuf) rs[m][t] = buf_rsrc(base[m][t], tb);
                 } else {
                     const int row = min(tile * kTileRows + i, rc - 1);
                     base[m][t] = W[m] + (size_t)row * rb_ * T::kBlockBytes;
@@ -571,7 +616,10 @@ struct UnitStream {
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
-                if constexpr (LAYOUT == M27Q_LAYOUT_TILED)
+                if constexpr (kBuf)
+                    f[m][t] = T::template load_tiled_buf<NT ? 2 : 0>(rs[m][t], (uint32_t)u * (uint32_t)T::kUnitBytes,
+                                                                     i, c, L);
+                else if constexpr (kTiled)
                     f[m][t] = T::template load_tiled<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
                 else
                     f[m][t] = T::template load_gguf<NT>(base[m][t], u, rb, c, L);
