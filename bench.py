@@ -11,9 +11,11 @@ in dependency order; every product quantizes its fp32 input inside the
 kernel.  A step is one such layer pass.  Weights rotate over enough distinct
 device copies (>= 2 x the 256 MB Infinity Cache) that every step streams its
 weights from HBM; a warm (cache-resident) figure is reported beside it.  The
-passes replay from HIP graphs of 32 layer passes each, as a decode step
-replays one graph for all its layers.  Before the W warmup passes, 100 ms of
-untimed layer passes let the GPU's clocks settle; each product timed alone
+K timed passes replay from one HIP graph of exactly K layer passes (past
+1024 passes, 1024-pass graphs and one for the rest), as a decode step
+replays one graph for all its layers.  Before the W warmup passes
+(their own graph), 100 ms of untimed layer passes let the GPU's clocks
+settle; each product timed alone
 rotates over copies of its own weights (>= 2 x the Infinity Cache) after 30 ms
 of untimed replays.
 
@@ -204,7 +206,7 @@ def rand_weight(m27q, torch, dev, t, rc, k, layout=None):
         raw[:, 209] = 0x0a
     else:
         raw[:, 1] = 0x0a
-        if t == m27q.Q4_K:
+        if t in (m27q.Q4_K, m27q.Q5_K):
             raw[:, 3] = 0x0a
     if layout == m27q.GGUF:
         return m27q.Weight(raw.reshape(-1), t, rb, rc, layout)
@@ -241,7 +243,7 @@ def timed(torch, fn, ncopies, reps, warm=3, calls=32):
     return time_graph(torch, g, max(1, reps // rot)) / (rot * ncopies) * 1e3
 
 
-SECTIONS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "decode")
+SECTIONS = ("cfg1", "cfg2", "cfg3", "types", "cfg4", "cfg5", "decode")
 
 
 def suite(m27q, torch, dev, layers, host, reps, sections=SECTIONS):
@@ -276,6 +278,25 @@ def suite(m27q, torch, dev, layers, host, reps, sections=SECTIONS):
         del pool
         out["cfg1_q4k_17408x5120_m1"] = {"us": round(us, 3), "GBps": round(50135040 / us / 1e3, 1)}
         log(f"config 1: {us:.2f} us")
+    # the further weight types at the shapes the reference's UD-Q4_K_XL file
+    # gives them: the SSM layer's pair on one activation (l_mv_pair,
+    # exec:2106-2125: wqkv Q6_K 10240 x 5120 and wqkv_gate Q5_K 6144 x 5120,
+    # one launch per type), Q5_K alone, and IQ4_XS at the FFN's 17408 x 5120
+    if "types" in sections:
+        for key, spec in (("ssm_pair_q6k_10240_q5k_6144_x5120_m1", ((m27q.Q6_K, 10240), (m27q.Q5_K, 6144))),
+                          ("q5k_6144x5120_m1", ((m27q.Q5_K, 6144),)),
+                          ("iq4xs_17408x5120_m1", ((m27q.IQ4_XS, 17408),))):
+            nbytes = sum(rc * 20 * m27q.BLOCK_BYTES[t] for t, rc in spec)
+            nc = max(2, -(-2 * MALL_BYTES // nbytes) + 1)
+            ws = [[rand_weight(m27q, torch, dev, t, rc, 5120) for t, rc in spec] for _ in range(nc)]
+            ys = [torch.empty(rc, dtype=torch.float32, device=dev) for _, rc in spec]
+            if len(spec) == 1:
+                us = timed(torch, lambda c, st: m27q.matvec(ws[c][0], x5120, ys[0], stream=st), nc, reps)
+            else:
+                us = timed(torch, lambda c, st: m27q.matvec_multi(ws[c], x5120, ys, stream=st), nc, reps)
+            out[key] = {"us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
+            log(f"{key}: {us:.2f} us")
+            del ws
     # config 2: Q8_0 draft shapes, fp32 x
     for rc, k in ((2048, 2048), (6144, 2048), (2048, 6144)) if "cfg2" in sections else ():
         nbytes = rc * k // 32 * 34
@@ -397,7 +418,7 @@ def time_graph(torch, g, reps):
     return e0.elapsed_time(e1) / reps
 
 
-STREAM_SIZES_MB = (4.456, 13.37, 17.76, 23.65, 50.14, 73.22, 100.36, 200.0, 1000.0)
+STREAM_SIZES_MB = (4.456, 13.37, 17.76, 21.63, 23.65, 47.35, 50.14, 64.63, 73.22, 100.36, 200.0, 1000.0)
 
 
 def stream_lib():
@@ -411,7 +432,8 @@ def stream_lib():
 
 def stream_read_peak(torch, dev, reps):
     """GB/s of the plain streaming read at each size (the Q8_0 draft products'
-    sizes, the layer's product sizes, 200 MB and 1 GB), from HIP events over graph replays that rotate through
+    sizes, the layer's product sizes, the further weight types' products, 200
+    MB and 1 GB), from HIP events over graph replays that rotate through
     >= 2 x the 256 MB Infinity Cache of distinct bytes (each read streams from
     HBM).  Every launch includes its dispatch, as the products' figures do."""
     L = stream_lib()
@@ -552,7 +574,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true", help="skip the configurations other than the layer")
     ap.add_argument("--only", default="",
-                    help="comma-separated suite sections (cfg1,cfg2,cfg4,cfg5,decode) to run alone, without the "
+                    help="comma-separated suite sections (cfg1,cfg2,cfg3,types,cfg4,cfg5,decode) to run alone, without the "
                          "layer timing; prints their figures (for profiler runs), not the benchmark line")
     ap.add_argument("--timeline", action="store_true",
                     help="per-wave timeline of each M = 1 product from the measurement build "

@@ -62,6 +62,10 @@
 // (30.6 and 21.6 us against 24.2 and 16.4 TILED).
 #pragma once
 
+#include <cstdint>
+
+#include "m27q_layout.h"
+
 namespace m27q {
 
 template <int KS_, int TPW_, int WT_, int NT_ = 1>
@@ -86,15 +90,21 @@ static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallbac
 enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
-// multi-matrix launch) over upr units per row.
-inline int pick_gemv_cfg(bool /*tiled*/, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
+// multi-matrix launch) of one weight type over upr units per row.  Q6_K on an
+// fp32 x at 6144-12288 rows takes (4, 1, 1) where Q4_K takes (8, 4, 2): the
+// SSM layer's wqkv (Q6_K 10240 x 5120) measured 9.8 us against 12.9 (cold
+// copies, events); the other shapes measured within 0.3 us of each other or
+// slower for Q6_K, Q5_K 6144 x 5120 and IQ4_XS 17408 x 5120.
+inline int pick_gemv_cfg(uint32_t type, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
     if (out_quant) return kCfgQ;
     if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
     if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
         if (upr >= 24) return xf32 ? kCfg822 : kCfg81;
         if (!xf32) return kCfg41;
-        return rows_total <= 2048 ? kCfg161 : rows_total <= 6144 ? kCfg81 : kCfg84;
+        if (rows_total <= 2048) return kCfg161;
+        if (rows_total <= 6144) return kCfg81;
+        return type == kQ6_K ? kCfg41 : kCfg84;
     }
     return kCfg42;
 }
