@@ -69,6 +69,24 @@ __device__ __forceinline__ uint4 ld_u128_a2(const uint8_t *p) {
     return make_uint4(ld_u32_a2(p), ld_u32_a2(p + 4), ld_u32_a2(p + 8), ld_u32_a2(p + 12));
 }
 
+// The same 16 bytes from five dword loads: the 20 bytes from p rounded down
+// to a multiple of 4, shifted into place (v_alignbit_b32).  The caller
+// guarantees that those 20 bytes are readable (for GGUF Q6_K's ql and qh
+// chunks they lie inside the block: the next field follows).
+__device__ __forceinline__ uint4 ld_u128_a2w(const uint8_t *p) {
+    typedef uint32_t u4a4 __attribute__((ext_vector_type(4), aligned(4)));
+    // offset from p itself, so that the pointer keeps its global address space
+    // (through an integer it would become a flat pointer, and flat loads also
+    // count against the LDS wait counter)
+    const uint32_t mis = (uint32_t)((uintptr_t)p & 2);
+    const uint32_t *w = (const uint32_t *)(p - mis);
+    const uint32_t sh = mis * 8;  // 0 or 16 bits
+    const u4a4 v = *(const u4a4 *)w;
+    const uint32_t e = w[4];
+    return make_uint4(__builtin_amdgcn_alignbit(v.y, v.x, sh), __builtin_amdgcn_alignbit(v.z, v.y, sh),
+                      __builtin_amdgcn_alignbit(v.w, v.z, sh), __builtin_amdgcn_alignbit(e, v.w, sh));
+}
+
 // 16-byte load.  NT marks it non-temporal (global_load_dwordx4 ... nt), the
 // policy of the weight streams, which are read once per product: it keeps them
 // from displacing the activations and outputs other workgroups and the next
