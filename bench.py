@@ -260,16 +260,20 @@ def suite(m27q, torch, dev, layers, host, reps, sections=SECTIONS):
         us = timed(torch, lambda c, st: layer_pass(m27q, layers[c], B, st, STAGES_ATTN), len(layers), reps)
         out["cfg3_attention_layer_gated_wo"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
         log(f"attention layer (gated Wo): {us:.2f} us")
+    # the layer copies in GGUF layout, uploaded verbatim (config 3 and config 4)
+    gl = None
+    if "cfg3" in sections or "cfg4" in sections:
         first = {}
         for name, (t, rc, k, blocks) in host.items():
             first[name] = m27q.Weight.upload(blocks.reshape(-1), t, k // 256, rc, m27q.GGUF, dev)
         gl = [first] + [{n: m27q.Weight(w.data.clone(), w.type, w.rb, w.rc, w.layout) for n, w in first.items()}
                         for _ in range(1, len(layers))]
+        del first
         torch.cuda.synchronize()
+    if "cfg3" in sections:
         us = timed(torch, lambda c, st: layer_pass(m27q, gl[c], B, st), len(gl), reps)
         out["cfg3_layer_gguf_layout"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
         log(f"layer on GGUF-layout weights: {us:.2f} us")
-        del gl, first
     # config 1: Q4_K 17408 x 5120 alone, fp32 x
     if "cfg1" in sections:
         y = torch.empty(17408, dtype=torch.float32, device=dev)
@@ -316,12 +320,16 @@ def suite(m27q, torch, dev, layers, host, reps, sections=SECTIONS):
             m27q.quant_act(torch.from_numpy(rng.standard_normal((M, k)).astype(np.float32)).to(dev), a)
         Ys = {n: torch.empty((M, rc), dtype=torch.float32, device=dev) for n, _, rc, _ in LAYER}
 
-        def layer_m(c, st):
+        def layer_m(c, st, L=layers):
             for fn in STAGES_M.values():
-                fn(m27q, layers[c], acts, Ys, st)
+                fn(m27q, L[c], acts, Ys, st)
         us = timed(torch, layer_m, len(layers), reps)
         out[f"cfg4_layer_m{M}"] = {"us": round(us, 3), "GBps": round(LAYER_BYTES / us / 1e3, 1)}
-        log(f"config 4 M={M}: {us:.2f} us")
+        # the same on the GGUF-layout copies
+        us_g = timed(torch, lambda c, st: layer_m(c, st, gl), len(gl), reps)
+        out[f"cfg4_layer_m{M}_gguf_layout"] = {"us": round(us_g, 3), "GBps": round(LAYER_BYTES / us_g / 1e3, 1)}
+        log(f"config 4 M={M}: {us:.2f} us, GGUF layout {us_g:.2f} us")
+    del gl
     # config 5: LM head GEMV, exact top-64, 512-row gather
     if "cfg5" in sections or "decode" in sections:
         lm = rand_weight(m27q, torch, dev, m27q.Q6_K, 248320, 5120)

@@ -253,18 +253,20 @@ M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float
  * K) bytes: Q8_0 weights whose K is not a multiple of 128 read up to 96 bytes
  * past the last row's codes); Y is [M][row_count].  TILED weights run on the
  * GEMV structure for M = 2 and on int8 MFMA (v_mfma_i32_16x16x32_i8, up to 16
- * activation rows per launch) from M = 3; GGUF weights on a packed-int8-dot
- * path; M = 1 is m27q_matvec_q8.  No reference
+ * activation rows per launch) from M = 3; GGUF-layout Q4_K / Q5_K / Q6_K
+ * weights on int8 MFMA from M = 2, other GGUF-layout weights on a
+ * packed-int8-dot path; M = 1 is m27q_matvec_q8.  No reference
  * counterpart: the reference runs prefill and decode one token at a time
  * (src/mono27b_chat.cpp:399-403); results equal M independent M = 1 products
  * up to fp32 rounding. */
 M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq, float *Y,
                                     const float *residual, hipStream_t stream);
 
-/* Up to 4 TILED weights of one K on the same M activation rows: Ys[i] = X
- * W[i]^T ([M][row_count_i] each), one launch per weight type as in
- * m27q_matvec_q8_multi.  The small-M counterpart of m27q_matvec_q8_multi
- * (q/k/v, gate/up of a verify batch). */
+/* Up to 4 weights of one K on the same M activation rows: Ys[i] = X W[i]^T
+ * ([M][row_count_i] each), one launch per (type, layout) group as in
+ * m27q_matvec_q8_multi (GGUF-layout Q8_0 / IQ4_XS: one launch per weight).
+ * The small-M counterpart of m27q_matvec_q8_multi (q/k/v, gate/up of a
+ * verify batch). */
 M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
                                           hipStream_t stream);
 

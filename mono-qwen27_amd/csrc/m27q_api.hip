@@ -194,11 +194,14 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     return hip_status(e);
 }
 
-// Small-M products for TILED weights: up to kMtMaxM tokens on the GEMV
+// Small-M products: for TILED weights, up to kMtMaxM tokens on the GEMV
 // streaming structure when their activations fit the LDS budget
 // (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).  Measured on the
 // Qwen-27B layer: 56 us against 63 at M = 2; from M = 3 on the MFMA kernel
 // with two row sets per tile is faster (63 against 75 us at M = 4).
+// GGUF-layout Q4_K / Q5_K / Q6_K weights take the MFMA kernel from M = 2 on
+// (staged from the row blocks); GGUF-layout Q8_0 and IQ4_XS weights, one
+// launch per matrix of the VALU kernel (m27q_matmul.hip).
 constexpr int kMtMaxM = 2;
 constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU
 
@@ -209,23 +212,49 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
         if (st != M27Q_OK) return st;
         if (!Ys[i]) return M27Q_ERR_NULL;
         if (ws[i].ggml_type != ws[0].ggml_type) return M27Q_ERR_TYPE;
-        if (ws[i].layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
+        if (ws[i].layout != ws[0].layout) return M27Q_ERR_LAYOUT;
         if (ws[i].row_blocks != ws[0].row_blocks) return M27Q_ERR_SHAPE;
     }
     if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
+    const uint32_t type = ws[0].ggml_type;
+    const int layout = (int)ws[0].layout;
+    const bool tiled = layout == M27Q_LAYOUT_TILED;
     MatmulMultiParams p{};
-    p.upr = units_per_row(ws[0].ggml_type, ws[0].row_blocks);
+    p.upr = units_per_row(type, ws[0].row_blocks);
     p.K = k_of(&ws[0]);
     p.M = M;
-    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(ws[0].ggml_type, p.upr) <= kMtLdsBudget;
-    if (!few && matmul_mfma_lds_bytes(ws[0].ggml_type) > lds_limit()) return M27Q_ERR_SHAPE;
+    const ActView a = act_view(xq, M, p.K);
+    if (!matmul_mfma_takes(type, layout)) {  // GGUF Q8_0 / IQ4_XS
+        if (dry) return M27Q_OK;
+        for (int i = 0; i < n; ++i) {
+            MatmulParams q{};
+            q.W = (const uint8_t *)ws[i].ptr;
+            q.rb = (int)ws[i].row_blocks;
+            q.rc = (int)ws[i].row_count;
+            q.upr = p.upr;
+            q.K = p.K;
+            q.M = M;
+            q.xq = a.q;
+            q.xd = a.d;
+            q.xs = a.s;
+            q.Y = Ys[i];
+            q.res = res[i];
+            const hipError_t e = launch_matmul_q8(type, layout, q, stream);
+            if (e != hipSuccess) return hip_status(e);
+        }
+        return M27Q_OK;
+    }
+    const bool few = tiled && M <= kMtMaxM && matmul_mt_lds_bytes(type, p.upr) <= kMtLdsBudget;
+    if (!few && matmul_mfma_lds_bytes(type) > lds_limit()) return M27Q_ERR_SHAPE;
     // The MFMA kernel reads each matrix through a buffer descriptor with a
     // 32-bit size; the activations (M <= kMaxM rows of K <= kMaxK) stay far
     // below it.
-    for (int i = 0; i < n && !few; ++i)
-        if (tiled_bytes(ws[i].ggml_type, ws[i].row_blocks, ws[i].row_count) >= (1ull << 32)) return M27Q_ERR_SHAPE;
+    for (int i = 0; i < n && !few; ++i) {
+        const size_t wb = tiled ? tiled_bytes(type, ws[i].row_blocks, ws[i].row_count)
+                                : (size_t)ws[i].row_blocks * ws[i].row_count * (size_t)block_bytes(type);
+        if (wb >= (1ull << 32)) return M27Q_ERR_SHAPE;
+    }
     if (dry) return M27Q_OK;
-    const ActView a = act_view(xq, M, p.K);
     p.xq = a.q;
     p.xd = a.d;
     p.xs = a.s;
@@ -237,8 +266,7 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
         p.res[i] = res[i];
         p.rc[i] = (int)ws[i].row_count;
     }
-    return hip_status(few ? launch_matmul_mt(ws[0].ggml_type, p, stream)
-                          : launch_matmul_mfma(ws[0].ggml_type, p, stream));
+    return hip_status(few ? launch_matmul_mt(type, p, stream) : launch_matmul_mfma(type, layout, p, stream));
 }
 
 // Up to kMaxMulti weights of one K sharing one activation, of any mix of
@@ -388,34 +416,16 @@ M27Q_API m27q_status m27q_matmul_q8(const m27q_weight *w, int M, const void *xq,
     if (!xq || !Y) return M27Q_ERR_NULL;
     if (M < 1 || M > kMaxM) return M27Q_ERR_SHAPE;
     if (!aligned(xq, 16)) return M27Q_ERR_LAYOUT;
-    MatmulParams p{};
-    p.W = (const uint8_t *)w->ptr;
-    p.rb = (int)w->row_blocks;
-    p.rc = (int)w->row_count;
-    p.upr = units_per_row(w->ggml_type, w->row_blocks);
-    p.K = k_of(w);
-    p.M = M;
-    const ActView a = act_view(xq, M, p.K);
-    p.xq = a.q;
-    p.xd = a.d;
-    p.xs = a.s;
-    p.Y = Y;
-    p.res = residual;
     if (M == 1) return m27q_matvec_q8(w, xq, Y, residual, nullptr, stream);
-    if (w->layout == M27Q_LAYOUT_TILED) {
-        float *Ys[1] = {Y};
-        const float *rs[1] = {residual};
-        return matmul_multi_impl(1, w, M, xq, Ys, rs, stream);
-    }
-    return hip_status(launch_matmul_q8(w->ggml_type, (int)w->layout, p, stream));
+    float *Ys[1] = {Y};
+    const float *rs[1] = {residual};
+    return matmul_multi_impl(1, w, M, xq, Ys, rs, stream);
 }
 
 M27Q_API m27q_status m27q_matmul_q8_multi(int n, const m27q_weight *ws, int M, const void *xq, float *const *Ys,
                                           hipStream_t stream) {
     if (!ws || !Ys || !xq) return M27Q_ERR_NULL;
     if (n < 1 || n > kMaxMulti || M < 1 || M > kMaxM) return M27Q_ERR_SHAPE;
-    for (int i = 0; i < n; ++i)
-        if (ws[i].layout != M27Q_LAYOUT_TILED) return M27Q_ERR_LAYOUT;
     if (M == 1) return m27q_matvec_q8_multi(n, ws, xq, Ys, stream);
     return grouped_multi(n, ws, M, xq, nullptr, Ys, stream);
 }

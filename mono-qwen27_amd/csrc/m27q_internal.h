@@ -108,12 +108,14 @@ hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hi
 size_t matmul_mt_lds_bytes(uint32_t type, int upr);
 int matmul_mt_balance(long long tiles, int upr, int cus);
 hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
-// int8-MFMA small-M products (m27q_mma.hip): TILED weights, any M (16 tokens
-// per launch).
+// int8-MFMA small-M products (m27q_mma.hip): TILED weights of every type and
+// GGUF-layout Q4_K / Q5_K / Q6_K (matmul_mfma_takes), any M (16 tokens per
+// launch).
 size_t matmul_mfma_lds_bytes(uint32_t type);
+bool matmul_mfma_takes(uint32_t type, int layout);
 // The current device's CU count and LDS bytes per workgroup (cached per device).
 int cu_count();
 size_t lds_limit();
-hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
+hipError_t launch_matmul_mfma(uint32_t type, int layout, const MatmulMultiParams &p, hipStream_t s);
 
 }  // namespace m27q

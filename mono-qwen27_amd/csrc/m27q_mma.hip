@@ -149,6 +149,16 @@ struct MmQ4KT {
         if (c < 72) return (8 * t + ((c - 8) >> 3)) * kRowBytes + 16 + 16 * ((c - 8) & 7);
         return (8 * t + ((c - 72) >> 1)) * kRowBytes + 144 + 16 * ((c - 72) & 1);  // Q5_K qh
     }
+    // GGUF layout: a row's block of the unit is kGgufChunks 16-byte chunks
+    // (Q4_K: header | qs, the record itself; Q5_K: header | qh | qs).
+    static constexpr int kBlockBytes = Q5 ? kQ5KBytes : kQ4KBytes;
+    static constexpr int kGgufChunks = kBlockBytes / 16;
+    static constexpr bool kGgufA2 = false;  // blocks are 16-byte aligned
+    __device__ static int gguf_dst(int j, int c) {
+        if (!Q5 || c == 0) return j * kRowBytes + 16 * c;
+        if (c < 3) return j * kRowBytes + 144 + 16 * (c - 1);  // qh
+        return j * kRowBytes + 16 + 16 * (c - 3);                // qs
+    }
     template <int PK>
     __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int) {
         constexpr int W8 = Pack<PK>::W8;
@@ -245,6 +255,13 @@ struct MmQ6K {
         if (c < 104) return (8 * t + (c - 96)) * kRowBytes + 192;
         return side + 16 * t;
     }
+    // GGUF layout: ql | qh | scales are the block's first 13 chunks, in the
+    // record's order; d (bytes 208-209) is staged apart into the side area.
+    // The 210-byte blocks leave the chunks 2-byte aligned (kGgufA2).
+    static constexpr int kBlockBytes = kQ6KBytes;
+    static constexpr int kGgufChunks = 13;
+    static constexpr bool kGgufA2 = true;
+    __device__ static int gguf_dst(int j, int c) { return j * kRowBytes + 16 * c; }
     template <int PK>
     __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int side) {
         constexpr int W8 = Pack<PK>::W8;
@@ -321,6 +338,10 @@ struct MmQ80 {
     static constexpr int kUnitBytes = kQ80Unit;
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
+    // TILED only (34-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
+    static constexpr int kBlockBytes = kQ80Bytes, kGgufChunks = 0;
+    static constexpr bool kGgufA2 = false;
+    __device__ static int gguf_dst(int, int) { return 0; }
     template <int PK>
     static constexpr int kPieces = PK;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
@@ -375,6 +396,10 @@ struct MmIQ4XS {
     static constexpr int kUnitBytes = kIQ4XSUnit;
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
+    // TILED only (136-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
+    static constexpr int kBlockBytes = kIQ4XSBytes, kGgufChunks = 0;
+    static constexpr bool kGgufA2 = false;
+    __device__ static int gguf_dst(int, int) { return 0; }
     template <int PK>
     static constexpr int kPieces = PK;
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
@@ -510,10 +535,28 @@ template <class T, int PK>
 constexpr int mm_waves_per_eu() {
     return (PK == 2 ? 3 : 4) - (T::kWide ? 1 : 0);
 }
-template <class T, int PK, int KS>
+// GGUF-layout weights (LAYOUT == M27Q_LAYOUT_GGUF; Q4_K, Q5_K and Q6_K): the
+// same LDS records, staged from each row's block of the unit (row_blocks ==
+// units per row for these types).  Rows past the matrix's end reread its last
+// row.  Temporal loads: a row's consecutive blocks share 128-byte lines.
+// Q6_K's 2-byte-aligned chunks are read as 20 bytes from the 4-aligned offset
+// below them and shifted into place; every read is inside the buffer's range
+// or, past it, a buffer load that returns zeros.
+template <int AUX>
+__device__ __forceinline__ uint32_t buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return bld_u32<AUX>(r, voff, soff);
+}
+__device__ __forceinline__ v4u shift16(const v4u &v, uint32_t e, uint32_t sh) {
+    return v4u{__builtin_amdgcn_alignbit(v.y, v.x, sh), __builtin_amdgcn_alignbit(v.z, v.y, sh),
+               __builtin_amdgcn_alignbit(v.w, v.z, sh), __builtin_amdgcn_alignbit(e, v.w, sh)};
+}
+
+template <class T, int PK, int KS, int LAYOUT>
 __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmul_mfma(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     using SG = Stage<T, PK>;
+    constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;
+    static_assert(!kG || 16 * PK * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
     constexpr int G = T::kGroups, NS = T::kSteps, TK = Pack<PK>::TK, UE = SG::UE, UB = SG::UB;
     constexpr int CPU = UB / 16;  // chunks per tile unit
     const int lane = (int)(threadIdx.x & 63);
@@ -544,15 +587,27 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     // zeros; their groups have zero scales.
     uint32_t goff[SG::kNW];
     int wdst[SG::kNW];
+    constexpr int UBW = kG ? T::kBlockBytes : UB;  // weight bytes of one unit per tile (GGUF: per row)
+    const uint32_t rowb = (uint32_t)p.upr * (uint32_t)T::kBlockBytes;  // GGUF row bytes
 #pragma unroll
     for (int n = 0; n < SG::kNW; ++n) {
         const int id = n * kWave + lane;
-        const bool ok = id < SG::kWChunks;
-        const int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
-        const int tile = min(row0 / kTileRows + t, ntiles8 - 1);
-        goff[n] = (uint32_t)tile * (uint32_t)(p.upr * UB) + 16u * c;
-        wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
+        if constexpr (kG) {
+            const bool ok = id < 16 * PK * T::kGgufChunks;
+            const int j = ok ? id / T::kGgufChunks : 0, c = ok ? id % T::kGgufChunks : 0;
+            goff[n] = (uint32_t)min(row0 + j, rc - 1) * rowb + 16u * c;
+            wdst[n] = ok ? T::gguf_dst(j, c) : SG::oDummy;
+        } else {
+            const bool ok = id < SG::kWChunks;
+            const int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
+            const int tile = min(row0 / kTileRows + t, ntiles8 - 1);
+            goff[n] = (uint32_t)tile * (uint32_t)(p.upr * UB) + 16u * c;
+            wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
+        }
     }
+    // GGUF Q6_K: lanes 0 .. 16 PK - 1 stage the d of row `lane` of the set
+    const uint32_t doff = (uint32_t)min(row0 + (lane & (16 * PK - 1)), rc - 1) * rowb + (uint32_t)kQ6KD;
+    const int ddst = lane < 16 * PK ? SG::kSide + 16 * (lane >> 3) + 2 * (lane & 7) : SG::oDummy;
     uint32_t aoff[SG::kNA];
     int adst[SG::kNA];
 #pragma unroll
@@ -567,16 +622,30 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     const bool s_tok_in = s_on && s_tok < Mloc;
     const uint32_t s_row = (uint32_t)(m0 + (s_tok_in ? s_tok : 0)) * (uint32_t)ngroups + 4u * s_h;
 
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(Wm, (uint32_t)ntiles8 * (uint32_t)(p.upr * UB));
+    const __amdgpu_buffer_rsrc_t wr =
+        buf_rsrc(Wm, kG ? (uint32_t)rc * rowb : (uint32_t)ntiles8 * (uint32_t)(p.upr * UB));
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(p.xq, (uint32_t)p.M * (uint32_t)p.K);
     const uint32_t sbytes = (uint32_t)p.M * (uint32_t)ngroups * 4u;
     const __amdgpu_buffer_rsrc_t dr = buf_rsrc(p.xd, sbytes), sr = buf_rsrc(p.xs, sbytes);
+    constexpr bool kA2 = kG && T::kGgufA2;
     v4u rw[SG::kNW], ra[SG::kNA];
+    uint32_t re[kA2 ? SG::kNW : 1], rsh[kA2 ? SG::kNW : 1], rd = 0u;
     float sd[4];
     uint32_t ss[4] = {0u, 0u, 0u, 0u};
     auto issue = [&](int u) __attribute__((always_inline)) {
+        if constexpr (kA2) {
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) rw[n] = buf_ld16<kWeightAux>(wr, goff[n], (uint32_t)u * UB);
+            for (int n = 0; n < SG::kNW; ++n) {
+                const uint32_t v = goff[n] + (uint32_t)u * UBW, a = v & ~3u;
+                rw[n] = buf_ld16(wr, a, 0u);
+                re[n] = buf_ld4<0>(wr, a + 16u, 0u);
+                rsh[n] = (v & 2u) * 8u;
+            }
+            rd = bld_u16(wr, doff, (uint32_t)u * UBW);
+        } else {
+#pragma unroll
+            for (int n = 0; n < SG::kNW; ++n) rw[n] = buf_ld16<kG ? 0 : kWeightAux>(wr, goff[n], (uint32_t)u * UBW);
+        }
 #pragma unroll
         for (int n = 0; n < SG::kNA; ++n) ra[n] = buf_ld16(xr, aoff[n], (uint32_t)u * UE);
         if constexpr (G == 8) {  // whole units: rows of 8 k groups, 16-byte aligned
@@ -598,8 +667,14 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
         }
     };
     auto commit = [&](int u) __attribute__((always_inline)) {
+        if constexpr (kA2) {
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+            for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = shift16(rw[n], re[n], rsh[n]);
+            *(uint16_t *)(wl + ddst) = (uint16_t)rd;
+        } else {
+#pragma unroll
+            for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+        }
 #pragma unroll
         for (int n = 0; n < SG::kNA; ++n) *(v4u *)(wl + adst[n]) = ra[n];
         float *dT = (float *)(wl + SG::oS), *aT = dT + G * TK;
@@ -727,11 +802,13 @@ struct XStage {
 // 16-byte activation chunks each thread has in flight while staging: 16
 // tokens x 6144 codes / 1024 threads in one round.
 constexpr int kXBatch = 6;
-template <class T, int NWV>
+template <class T, int NWV, int LAYOUT>
 __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     using XS = XStage<T>;
     using SG = typename XS::SG;
+    constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;  // as in k_matmul_mfma
+    static_assert(!kG || 16 * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
     constexpr int G = T::kGroups, NS = T::kSteps, TK = 16, UE = SG::UE, UB = SG::UB;
     constexpr int CPU = UB / 16;
     constexpr int NP = T::template kPieces<1>;
@@ -788,16 +865,28 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
 
     // Weight staging map of this lane (the same for every set; tiles past the
     // matrix's end reread its last tile).
+    // (GGUF: wt = the row within the set, wc = the chunk of its block)
     int wdst[SG::kNW], wt[SG::kNW], wc[SG::kNW];
 #pragma unroll
     for (int n = 0; n < SG::kNW; ++n) {
         const int id = n * kWave + lane;
-        const bool ok = id < SG::kWChunks;
-        wt[n] = ok ? id / CPU : 0;
-        wc[n] = ok ? id % CPU : 0;
-        wdst[n] = ok ? T::lds_dst(wt[n], wc[n], SG::kSide) : XS::oDummy;
+        if constexpr (kG) {
+            const bool ok = id < 16 * T::kGgufChunks;
+            wt[n] = ok ? id / T::kGgufChunks : 0;
+            wc[n] = ok ? id % T::kGgufChunks : 0;
+            wdst[n] = ok ? T::gguf_dst(wt[n], wc[n]) : XS::oDummy;
+        } else {
+            const bool ok = id < SG::kWChunks;
+            wt[n] = ok ? id / CPU : 0;
+            wc[n] = ok ? id % CPU : 0;
+            wdst[n] = ok ? T::lds_dst(wt[n], wc[n], SG::kSide) : XS::oDummy;
+        }
     }
+    constexpr bool kA2 = kG && T::kGgufA2;
+    const uint32_t rowb = (uint32_t)upr * (uint32_t)T::kBlockBytes;  // GGUF row bytes
+    const int ddst = lane < 16 ? SG::kSide + 16 * (lane >> 3) + 2 * (lane & 7) : XS::oDummy;
     v4u rw[SG::kNW];
+    uint32_t re[kA2 ? SG::kNW : 1], rsh[kA2 ? SG::kNW : 1], rd = 0u;
     auto issue = [&](int idx) __attribute__((always_inline)) {
         const int gs = s0 + idx / upr, u = idx % upr;
         int mi = 0;
@@ -805,17 +894,43 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
         for (int k = 1; k < kMaxMulti; ++k)
             if (k < p.nmat && gs >= p.wg_start[k]) mi = k;
         const int rc = p.rc[mi], ntiles8 = (rc + kTileRows - 1) / kTileRows;
-        const int tile0 = (gs - p.wg_start[mi]) * 2;
-        const __amdgpu_buffer_rsrc_t wr = buf_rsrc(p.W[mi], (uint32_t)ntiles8 * (uint32_t)(upr * UB));
+        if constexpr (kG) {
+            const int row0 = (gs - p.wg_start[mi]) * 16;
+            const __amdgpu_buffer_rsrc_t wr = buf_rsrc(p.W[mi], (uint32_t)rc * rowb);
+            const uint32_t ub = (uint32_t)u * (uint32_t)T::kBlockBytes;
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) {
-            const int tile = min(tile0 + wt[n], ntiles8 - 1);
-            rw[n] = buf_ld16<kWeightAux>(wr, (uint32_t)tile * (uint32_t)(upr * UB) + 16u * (uint32_t)wc[n], (uint32_t)u * UB);
+            for (int n = 0; n < SG::kNW; ++n) {
+                const uint32_t v = (uint32_t)min(row0 + wt[n], rc - 1) * rowb + 16u * (uint32_t)wc[n] + ub;
+                if constexpr (kA2) {
+                    const uint32_t a = v & ~3u;
+                    rw[n] = buf_ld16(wr, a, 0u);
+                    re[n] = buf_ld4<0>(wr, a + 16u, 0u);
+                    rsh[n] = (v & 2u) * 8u;
+                } else {
+                    rw[n] = buf_ld16(wr, v, 0u);
+                }
+            }
+            if constexpr (kA2) rd = bld_u16(wr, (uint32_t)min(row0 + (lane & 15), rc - 1) * rowb + (uint32_t)kQ6KD, ub);
+        } else {
+            const int tile0 = (gs - p.wg_start[mi]) * 2;
+            const __amdgpu_buffer_rsrc_t wr = buf_rsrc(p.W[mi], (uint32_t)ntiles8 * (uint32_t)(upr * UB));
+#pragma unroll
+            for (int n = 0; n < SG::kNW; ++n) {
+                const int tile = min(tile0 + wt[n], ntiles8 - 1);
+                rw[n] = buf_ld16<kWeightAux>(wr, (uint32_t)tile * (uint32_t)(upr * UB) + 16u * (uint32_t)wc[n],
+                                             (uint32_t)u * UB);
+            }
         }
     };
     auto commit = [&]() __attribute__((always_inline)) {
+        if constexpr (kA2) {
 #pragma unroll
-        for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+            for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = shift16(rw[n], re[n], rsh[n]);
+            *(uint16_t *)(wl + ddst) = (uint16_t)rd;
+        } else {
+#pragma unroll
+            for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = rw[n];
+        }
     };
 
     const int wrow = L.c;  // the lane's weight row within the set
@@ -919,7 +1034,7 @@ static size_t mfma_lds() {
     return (size_t)KS * Stage<T, PK>::kBytes;
 }
 
-template <class T, int PK, int KS>
+template <class T, int PK, int KS, int LAYOUT>
 static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
     const size_t lds = mfma_lds<T, PK, KS>();
     int total = 0;
@@ -928,7 +1043,7 @@ static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
         total += (p.rc[i] + 16 * PK - 1) / (16 * PK);
     }
     p.wg_start[p.nmat] = total;
-    hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
+    hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS, LAYOUT>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
     return hipGetLastError();
 }
 
@@ -945,8 +1060,8 @@ template <class T>
 constexpr int xres_waves() {
     return 16;
 }
-template <class T>
-static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *err) {
+template <class T, int LAYOUT>
+static bool launch_xres_t(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *err) {
     constexpr int NWV = xres_waves<T>();
     int S = 0;
     for (int i = 0; i < p.nmat; ++i) {
@@ -960,9 +1075,16 @@ static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *
     if (lds > lds_limit()) return false;
     // at most NWV sets per workgroup, so each wave's run covers at most two
     const int G = std::min(S, std::max(cus, (S + NWV - 1) / NWV));
-    hipLaunchKernelGGL((k_matmul_mfma_xres<T, NWV>), dim3(G), dim3(kWave * NWV), lds, s, p, m0);
+    hipLaunchKernelGGL((k_matmul_mfma_xres<T, NWV, LAYOUT>), dim3(G), dim3(kWave * NWV), lds, s, p, m0);
     *err = hipGetLastError();
     return true;
+}
+// GGUF-layout Q6_K's shifted chunk loads do not fit the resident kernel's 128
+// registers without spilling: those launches take the per-unit kernel.
+template <class T, int LAYOUT>
+static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipError_t *err) {
+    if constexpr (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) return false;
+    else return launch_xres_t<T, LAYOUT>(p, m0, s, err);
 }
 
 // Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 16: a
@@ -974,15 +1096,15 @@ static bool launch_xres(MatmulMultiParams p, int m0, hipStream_t s, hipError_t *
 // and the product has at least 128 sets of 32 rows (every product of the
 // layer): down at M = 8 takes 21.7 us against 28.8 with one-set tiles.
 constexpr int kPk2MinSets = 128;
-template <class T, int PK>
+template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
     long long sets = 0;
     for (int i = 0; i < p.nmat; ++i) sets += (p.rc[i] + 16 * PK - 1) / (16 * PK);
     const int ks = (sets < 320 || (PK == 1 && p.K <= 6144)) ? 8 : 4;
-    return ks == 8 ? launch_mfma_t<T, PK, 8>(p, m0, s) : launch_mfma_t<T, PK, 4>(p, m0, s);
+    return ks == 8 ? launch_mfma_t<T, PK, 8, LAYOUT>(p, m0, s) : launch_mfma_t<T, PK, 4, LAYOUT>(p, m0, s);
 }
 
-template <class T>
+template <class T, int LAYOUT>
 static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
     long long sets32 = 0;
     for (int i = 0; i < p.nmat; ++i) sets32 += (p.rc[i] + 31) / 32;
@@ -991,9 +1113,9 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
         const bool pk2 = left <= 8 && sets32 >= kPk2MinSets;
         hipError_t e = hipSuccess;
         if (pk2)
-            e = launch_mfma_pk<T, 2>(p, m0, s);
-        else if (!launch_xres<T>(p, m0, s, &e))
-            e = launch_mfma_pk<T, 1>(p, m0, s);
+            e = launch_mfma_pk<T, 2, LAYOUT>(p, m0, s);
+        else if (!launch_xres<T, LAYOUT>(p, m0, s, &e))
+            e = launch_mfma_pk<T, 1, LAYOUT>(p, m0, s);
         if (e != hipSuccess) return e;
         m0 += pk2 ? Pack<2>::TK : Pack<1>::TK;
     }
@@ -1018,13 +1140,25 @@ size_t matmul_mfma_lds_bytes(uint32_t type) {
     }
 }
 
-hipError_t launch_matmul_mfma(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
+bool matmul_mfma_takes(uint32_t type, int layout) {
+    return layout == M27Q_LAYOUT_TILED || type == kQ4_K || type == kQ5_K || type == kQ6_K;
+}
+
+hipError_t launch_matmul_mfma(uint32_t type, int layout, const MatmulMultiParams &p, hipStream_t s) {
+    if (layout == M27Q_LAYOUT_GGUF) {
+        switch (type) {
+            case kQ4_K: return launch_mfma_cfg<MmQ4K, M27Q_LAYOUT_GGUF>(p, s);
+            case kQ5_K: return launch_mfma_cfg<MmQ5K, M27Q_LAYOUT_GGUF>(p, s);
+            case kQ6_K: return launch_mfma_cfg<MmQ6K, M27Q_LAYOUT_GGUF>(p, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (type) {
-        case kQ4_K: return launch_mfma_cfg<MmQ4K>(p, s);
-        case kQ5_K: return launch_mfma_cfg<MmQ5K>(p, s);
-        case kQ6_K: return launch_mfma_cfg<MmQ6K>(p, s);
-        case kQ8_0: return launch_mfma_cfg<MmQ80>(p, s);
-        case kIQ4_XS: return launch_mfma_cfg<MmIQ4XS>(p, s);
+        case kQ4_K: return launch_mfma_cfg<MmQ4K, M27Q_LAYOUT_TILED>(p, s);
+        case kQ5_K: return launch_mfma_cfg<MmQ5K, M27Q_LAYOUT_TILED>(p, s);
+        case kQ6_K: return launch_mfma_cfg<MmQ6K, M27Q_LAYOUT_TILED>(p, s);
+        case kQ8_0: return launch_mfma_cfg<MmQ80, M27Q_LAYOUT_TILED>(p, s);
+        case kIQ4_XS: return launch_mfma_cfg<MmIQ4XS, M27Q_LAYOUT_TILED>(p, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -46,6 +46,15 @@ CASES = [  # type, rows, K, M, layout
     # every type, padding tokens
     ("Q4_K", 32776, 512, 8, 1), ("Q6_K", 32776, 768, 5, 1), ("Q8_0", 32776, 160, 7, 1),
     ("Q5_K", 32776, 512, 3, 1), ("IQ4_XS", 32776, 512, 8, 1),
+    # GGUF-layout K-quants on the MFMA kernel, staged from the row blocks:
+    # from M = 2, two-set tiles with a partial last set, 16-token resident
+    # launches (Q6_K: the per-unit kernel) and padding tokens; Q6_K rows of an
+    # odd block count (K = 768, 2304: every other row starts 2 bytes past a
+    # multiple of 4) and the down shape
+    ("Q4_K", 6144, 5120, 2, 0), ("Q4_K", 8200, 512, 6, 0), ("Q4_K", 16390, 1024, 16, 0), ("Q4_K", 4100, 1024, 19, 0),
+    ("Q5_K", 6144, 5120, 2, 0), ("Q5_K", 8200, 512, 8, 0), ("Q5_K", 16390, 1024, 25, 0),
+    ("Q6_K", 24, 768, 2, 0), ("Q6_K", 8200, 768, 7, 0), ("Q6_K", 16390, 1024, 16, 0), ("Q6_K", 1030, 2304, 11, 0),
+    ("Q6_K", 5120, 17408, 16, 0), ("Q6_K", 33, 2304, 4, 0),
 ]
 
 
@@ -117,3 +126,36 @@ def test_matmul_multi_resident_vs_oracle(m27q, ora, dev, M, rows):
         for m in range(M):
             want, nrm = ora.gemv_act(m27q.Q4_K, wb, 4, rc, q[m], d[m], s[m])
             assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (rc, m)
+
+
+@pytest.mark.parametrize("M", [2, 9, 16])
+def test_matmul_multi_gguf_vs_oracle(m27q, ora, dev, M):
+    """GGUF-layout weights through the multi entry point: Q4_K q/k/v-shaped
+    weights in one MFMA launch, then a mixed group (Q6_K on the MFMA kernel,
+    Q8_0 on the per-weight VALU kernel) on the same activation; every token
+    row of each output against the integer-dot oracle."""
+    import torch
+    k = 1536
+    spec = [("Q4_K", 6144, 80), ("Q4_K", 1024, 81), ("Q4_K", 1024, 82)]
+    mixed = [("Q6_K", 1030, 83), ("Q8_0", 515, 84)]
+    X = np.random.default_rng(M + 11).standard_normal((M, k)).astype(np.float32)
+    act = m27q.Act(M, k, dev)
+    m27q.quant_act(to_dev(X, dev), act)
+    q, d, s = act_host(m27q, act)
+    for group in (spec, mixed):
+        wbs, ws, rbs = [], [], []
+        for name, rc, seed in group:
+            t = getattr(m27q, name)
+            rb = k // m27q.BLOCK_ELEMS[t]
+            wb = ora.synth_weights(t, rc, k, seed=seed)
+            wbs.append(wb)
+            rbs.append(rb)
+            ws.append(m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.GGUF, dev))
+        Ys = [torch.empty((M, rc), dtype=torch.float32, device=dev) for _, rc, _ in group]
+        say("matmul multi gguf", M, [g[0] for g in group])
+        m27q.matmul_q8_multi(ws, act, Ys)
+        for (name, rc, _), wb, rb, Y in zip(group, wbs, rbs, Ys):
+            got = to_host(Y).astype(np.float64)
+            for m in range(M):
+                want, nrm = ora.gemv_act(getattr(m27q, name), wb, rb, rc, q[m], d[m], s[m])
+                assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (name, rc, m)

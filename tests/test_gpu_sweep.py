@@ -57,26 +57,28 @@ def test_random_bytes_vs_oracle(m27q, ora, dev, seed):
 
 @pytest.mark.parametrize("seed", range(9000, 9006))
 def test_random_resident_vs_oracle(m27q, ora, dev, seed):
-    """Random type, 16400-20000 rows (ragged last set), small K, 16-40 tokens
-    (resident 16-token launches, then the remainder on the per-unit kernel),
-    one or two weights of one K; every token row against the oracle."""
+    """Random type and layout, 16400-20000 rows (ragged last set), small K,
+    16-40 tokens (resident 16-token launches, then the remainder on the
+    per-unit kernel; GGUF-layout Q8_0 / IQ4_XS on the VALU kernel), one or
+    two weights of one K; every token row against the oracle."""
     import torch
     r = np.random.default_rng(3000 + seed)
     t = TYPES[r.integers(len(TYPES))]
     k = int(128 * r.integers(2, 9)) if t == "Q8_0" else int(256 * r.integers(1, 5))
     M = int(r.integers(16, 41))
     n = int(r.integers(1, 3))
+    layout = m27q.GGUF if r.integers(2) else m27q.TILED
     mats = []
     for i in range(n):
         rc = int(r.integers(16400, 20001))
-        tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, m27q.TILED, seed + 100 * i)
+        tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, layout, seed + 100 * i)
         mats.append((tid, wb, rb, w, rc))
     X = r.standard_normal((M, k)).astype(np.float32)
     act = m27q.Act(M, k, dev)
     m27q.quant_act(to_dev(X, dev), act)
     q, d, s = act_host(m27q, act)
     Ys = [torch.empty((M, m[4]), dtype=torch.float32, device=dev) for m in mats]
-    say("sweep resident", seed, t, [m[4] for m in mats], k, M)
+    say("sweep resident", seed, t, [m[4] for m in mats], k, M, layout)
     if n == 1:
         m27q.matmul_q8(mats[0][3], act, Ys[0])
     else:
@@ -92,8 +94,6 @@ def run_case(m27q, ora, dev, seed, raw):
     import torch
     c = draw(seed)
     t, k, rc, M, layout, r = c["type"], c["k"], c["rc"], c["M"], c["layout"], c["r"]
-    if c["kind"] == 2 and M > 1:
-        layout = m27q.TILED  # multi-weight small-M launches take TILED weights
     tid, wb, rb, w = weight(m27q, ora, dev, t, rc, k, layout, seed, raw)
     X = r.standard_normal((M, k)).astype(np.float32)
     act = m27q.Act(M, k, dev)
