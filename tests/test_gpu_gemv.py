@@ -321,22 +321,25 @@ def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k, layout):
     assert np.array_equal(to_host(y0).view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("layout_name", ["TILED", "GGUF"])
 @pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
-@pytest.mark.parametrize("rc,units", [(4098, 24), (5117, 2), (5120, 68)])
-def test_single_product_edges_every_type(m27q, ora, dev, type_name, rc, units):
-    """Single TILED products around the balanced-tiling rule, every integer-dot
-    type: 513 tiles with a last tile of 2 rows (24 units), 640 tiles with a last
-    tile of 5 rows and a single unit pair (fewer units than K slices: waves
-    with nothing to stream), and the 68-unit down shape (balanced tiling on
-    quantized input).  The quantized-input and the fp32-input products, each
-    with a residual, against the integer-dot oracle (in-kernel quantization
-    gives the same codes), the rows past row_count untouched."""
+@pytest.mark.parametrize("rc,units", [(4098, 24), (5117, 2), (5120, 68), (1030, 9)])
+def test_single_product_edges_every_type(m27q, ora, dev, layout_name, type_name, rc, units):
+    """Single products around the balanced-tiling rule, every integer-dot type
+    and both layouts: 513 tiles with a last tile of 2 rows (24 units), 640
+    tiles with a last tile of 5 rows and a single unit pair (fewer units than
+    K slices: waves with nothing to stream), the 68-unit down shape (balanced
+    tiling on quantized input), and rows of an odd unit count (GGUF Q6_K: every
+    other row starts 2 bytes past a multiple of 4; one-tile waves read its
+    fields as shifted dwords).  The quantized-input and the fp32-input
+    products, each with a residual, against the integer-dot oracle (in-kernel
+    quantization gives the same codes), the rows past row_count untouched."""
     import torch
     t = getattr(m27q, type_name)
     k = units * (128 if type_name == "Q8_0" else 256)
     rb = k // m27q.BLOCK_ELEMS[t]
     wb = weights(ora, type_name, rc, k, 21)
-    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, m27q.TILED, dev)
+    w = m27q.Weight.upload(wb.reshape(-1), t, rb, rc, getattr(m27q, layout_name), dev)
     rng = np.random.default_rng(17)
     x = rng.standard_normal(k).astype(np.float32)
     res = rng.standard_normal(rc).astype(np.float32)
@@ -346,7 +349,7 @@ def test_single_product_edges_every_type(m27q, ora, dev, type_name, rc, units):
     guard = np.float32(-7.25)
     y0 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
     y1 = torch.full((rc + 8,), float(guard), dtype=torch.float32, device=dev)
-    say("single product edges", type_name, rc, k)
+    say("single product edges", layout_name, type_name, rc, k)
     m27q.matvec_q8(w, act, y1[:rc], residual=rd)
     q, d, s = ora.quant_act(x)
     want, nrm = ora.gemv_act(t, wb, rb, rc, q, d, s)
