@@ -156,8 +156,8 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     const bool bal = n == 1 && !swiglu && !yq && (!x || p.K >= 10240) && tiles0 > 2LL * cus &&
                      tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB) * cus;
     const int cfg = bal ? kCfgB
-                        : pick_gemv_cfg(ws[0].ggml_type, x != nullptr, swiglu, yq && !quant_after,
-                                        rows_total, p.upr);
+                        : pick_gemv_cfg(ws[0].ggml_type, ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu,
+                                        yq && !quant_after, rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
     if (dry) return M27Q_OK;
     if (x) {

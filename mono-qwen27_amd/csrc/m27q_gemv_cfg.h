@@ -90,17 +90,21 @@ static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallbac
 enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
-// multi-matrix launch) of one weight type over upr units per row.  Q6_K on an
-// fp32 x at 6144-12288 rows takes (4, 1, 1) where Q4_K takes (8, 4, 2): the
-// SSM layer's wqkv (Q6_K 10240 x 5120) measured 9.8 us against 12.9 (cold
-// copies, events); the other shapes measured within 0.3 us of each other or
-// slower for Q6_K, Q5_K 6144 x 5120 and IQ4_XS 17408 x 5120.
-inline int pick_gemv_cfg(uint32_t type, bool xf32, bool swiglu, bool out_quant, long long rows_total, int upr) {
+// multi-matrix launch) of one weight type and layout over upr units per row.
+// Q6_K on an fp32 x at 6144-12288 rows takes (4, 1, 1) where Q4_K takes
+// (8, 4, 2): the SSM layer's wqkv (Q6_K 10240 x 5120) measured 9.8 us against
+// 12.9 (cold copies, events); the other shapes measured within 0.3 us of each
+// other or slower for Q6_K, Q5_K 6144 x 5120 and IQ4_XS 17408 x 5120.  On
+// GGUF-layout weights o's shape (24-39 units, fp32 x) takes (4, 1, 1) too:
+// 7.0 us against 8.1 with (8, 2, 2); q/k/v, gate/up, down and the LM head
+// measured best with the TILED choices.
+inline int pick_gemv_cfg(uint32_t type, bool tiled, bool xf32, bool swiglu, bool out_quant, long long rows_total,
+                         int upr) {
     if (out_quant) return kCfgQ;
     if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
     if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
-        if (upr >= 24) return xf32 ? kCfg822 : kCfg81;
+        if (upr >= 24) return xf32 ? (tiled ? kCfg822 : kCfg41) : kCfg81;
         if (!xf32) return kCfg41;
         if (rows_total <= 2048) return kCfg161;
         if (rows_total <= 6144) return kCfg81;
