@@ -605,8 +605,13 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
             wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
         }
     }
+    // GGUF Q6_K (2-byte aligned base): the descriptor starts at the 4-aligned
+    // address at or below the matrix (inside its allocation, whose start is
+    // 256-byte aligned), and every offset carries the base's low bits, so
+    // the dword reads and shifts follow the absolute addresses.
+    const uint32_t blo = kG && T::kGgufA2 ? (uint32_t)((uintptr_t)Wm & 3u) : 0u;
     // GGUF Q6_K: lanes 0 .. 16 PK - 1 stage the d of row `lane` of the set
-    const uint32_t doff = (uint32_t)min(row0 + (lane & (16 * PK - 1)), rc - 1) * rowb + (uint32_t)kQ6KD;
+    const uint32_t doff = blo + (uint32_t)min(row0 + (lane & (16 * PK - 1)), rc - 1) * rowb + (uint32_t)kQ6KD;
     const int ddst = lane < 16 * PK ? SG::kSide + 16 * (lane >> 3) + 2 * (lane & 7) : SG::oDummy;
     uint32_t aoff[SG::kNA];
     int adst[SG::kNA];
@@ -622,8 +627,8 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
     const bool s_tok_in = s_on && s_tok < Mloc;
     const uint32_t s_row = (uint32_t)(m0 + (s_tok_in ? s_tok : 0)) * (uint32_t)ngroups + 4u * s_h;
 
-    const __amdgpu_buffer_rsrc_t wr =
-        buf_rsrc(Wm, kG ? (uint32_t)rc * rowb : (uint32_t)ntiles8 * (uint32_t)(p.upr * UB));
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(Wm - blo, kG ? blo + (uint32_t)rc * rowb
+                                                             : (uint32_t)ntiles8 * (uint32_t)(p.upr * UB));
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(p.xq, (uint32_t)p.M * (uint32_t)p.K);
     const uint32_t sbytes = (uint32_t)p.M * (uint32_t)ngroups * 4u;
     const __amdgpu_buffer_rsrc_t dr = buf_rsrc(p.xd, sbytes), sr = buf_rsrc(p.xs, sbytes);
@@ -636,7 +641,7 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
         if constexpr (kA2) {
 #pragma unroll
             for (int n = 0; n < SG::kNW; ++n) {
-                const uint32_t v = goff[n] + (uint32_t)u * UBW, a = v & ~3u;
+                const uint32_t v = blo + goff[n] + (uint32_t)u * UBW, a = v & ~3u;
                 rw[n] = buf_ld16(wr, a, 0u);
                 re[n] = buf_ld4<0>(wr, a + 16u, 0u);
                 rsh[n] = (v & 2u) * 8u;

@@ -159,3 +159,43 @@ def test_matmul_multi_gguf_vs_oracle(m27q, ora, dev, M):
             for m in range(M):
                 want, nrm = ora.gemv_act(getattr(m27q, name), wb, rb, rc, q[m], d[m], s[m])
                 assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (name, rc, m)
+
+
+@pytest.mark.parametrize("type_name,rc,k", [("Q6_K", 1030, 2304), ("Q6_K", 8200, 768), ("Q6_K", 4098, 6144),
+                                            ("Q8_0", 515, 1056)])
+def test_gguf_two_byte_aligned_base(m27q, ora, dev, type_name, rc, k):
+    """GGUF Q6_K and Q8_0 weights need only 2-byte alignment: the matrix placed
+    2 bytes past a multiple of 4 (a view into a larger buffer).  The M = 1
+    products (quantized and fp32 x; one- and two-tile waves read Q6_K's fields
+    as shifted dwords or halfwords) and the small-M products (Q6_K: the MFMA
+    kernel with one- and two-set tiles, whose staging reads dwords from the
+    4-aligned address below each chunk; Q8_0: the VALU kernel), every token
+    row against the integer-dot oracle."""
+    import torch
+    t = getattr(m27q, type_name)
+    rb = k // m27q.BLOCK_ELEMS[t]
+    wb = ora.synth_weights(t, rc, k, seed=90)
+    raw = torch.from_numpy(wb.reshape(-1).copy()).to(dev)
+    buf = torch.zeros(raw.numel() + 2, dtype=torch.uint8, device=dev)
+    buf[2:] = raw
+    w = m27q.Weight(buf[2:], t, rb, rc, m27q.GGUF)
+    assert w.data.data_ptr() % 4 == 2
+    rng = np.random.default_rng(91)
+    for M in (1, 2, 7, 16):
+        X = rng.standard_normal((M, k)).astype(np.float32)
+        act = m27q.Act(M, k, dev)
+        m27q.quant_act(to_dev(X, dev), act)
+        q, d, s = act_host(m27q, act)
+        Y = torch.empty((M, rc), dtype=torch.float32, device=dev)
+        say("gguf 2-byte base", type_name, rc, k, M)
+        m27q.matmul_q8(w, act, Y)
+        got = to_host(Y).astype(np.float64)
+        for m in range(M):
+            want, nrm = ora.gemv_act(t, wb, rb, rc, q[m], d[m], s[m])
+            assert (np.abs(got[m] - want) <= int_dot_tol(nrm)).all(), (M, m)
+        if M == 1:
+            y = torch.empty(rc, dtype=torch.float32, device=dev)
+            m27q.matvec(w, to_dev(X[0], dev), y)
+            qf, df, sf = ora.quant_act(X[0])
+            want, nrm = ora.gemv_act(t, wb, rb, rc, qf, df, sf)
+            assert (np.abs(to_host(y).astype(np.float64) - want) <= int_dot_tol(nrm)).all(), "fp32 x"
