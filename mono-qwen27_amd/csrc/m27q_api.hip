@@ -155,7 +155,14 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
     const int cus = cu_count();
     const bool bal = n == 1 && !swiglu && !yq && (!x || p.K >= 10240) && tiles0 > 2LL * cus &&
                      tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB) * cus;
-    const int cfg = bal ? kCfgB
+    // The same with 8 to 9 tiles per CU (config 1's Q4_K 17408 x 5120: 8.5),
+    // where the other shapes leave a fifth two-tile workgroup on a quarter of
+    // the CUs: 10.5 us against 11.1 on an fp32 x (cold copies, events), and
+    // x is staged 256 times instead of 1088.
+    const bool bal9 = n == 1 && !swiglu && !yq && tiles0 > 8LL * cus &&
+                      tiles0 <= (long long)gemv_q8_tiles_per_wg(kCfgB9) * cus;
+    const int cfg = bal9 ? kCfgB9
+                  : bal ? kCfgB
                         : pick_gemv_cfg(ws[0].ggml_type, ws[0].layout == M27Q_LAYOUT_TILED, x != nullptr, swiglu,
                                         yq && !quant_after, rows_total, p.upr);
     if (gemv_q8_lds_bytes(ws[0].ggml_type, p.upr, swiglu, cfg) > lds_limit()) return M27Q_ERR_SHAPE;
@@ -175,9 +182,9 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
         p.y[i] = ys[i];
         p.rc[i] = (int)ws[i].row_count;
         p.wg_start[i] = total;
-        total += bal ? cus : (tiles_of(ws[i].row_count) + tpw - 1) / tpw;
+        total += bal || bal9 ? cus : (tiles_of(ws[i].row_count) + tpw - 1) / tpw;
     }
-    p.bal = bal ? 1 : 0;
+    p.bal = bal || bal9 ? 1 : 0;
     if (swiglu) p.W[1] = (const uint8_t *)ws[1].ptr;
     else p.res[0] = residual;
     p.wg_start[nout] = total;

@@ -470,6 +470,9 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfgB:  // balanced tiling, single products without the SwiGLU epilogue only
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, CfgB, SWIGLU, XF32>(p, s);
             return hipErrorInvalidValue;
+        case kCfgB9:
+            if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, CfgB9, SWIGLU, XF32>(p, s);
+            return hipErrorInvalidValue;
         default: return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
     }
 }
@@ -502,6 +505,7 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
         case kCfg161: return swiglu ? lds_sw<T, Cfg41>(upr, swiglu) : lds_sw<T, Cfg161>(upr, swiglu);
         case kCfg822: return std::max(lds_sw<T, Cfg42>(upr, swiglu), lds_sw<T, Cfg822>(upr, swiglu));
         case kCfgB: return lds_sw<T, CfgB>(upr, swiglu);
+        case kCfgB9: return lds_sw<T, CfgB9>(upr, swiglu);
         default: return lds_sw<T, Cfg41>(upr, swiglu);
     }
 }
@@ -526,6 +530,7 @@ int gemv_q8_tiles_per_wg(int cfg) {
         case kCfg161: return Cfg161::TPW;
         case kCfg822: return Cfg822::TPW;
         case kCfgB: return CfgB::TPW;
+        case kCfgB9: return CfgB9::TPW;
         default: return Cfg41::TPW;
     }
 }

@@ -84,10 +84,12 @@ using CfgQ = GemvCfg<2, 4, 2, 1>;
 using Cfg161 = GemvCfg<16, 1, 1, 1>;
 using Cfg822 = GemvCfg<8, 2, 2, 0>;
 using CfgB = GemvCfg<4, 3, 1, 1>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
+using CfgB9 = GemvCfg<4, 9, 3, 1>;  // balanced tiling for 8-9 tiles per CU (config 1); swept against
+                                     // (5, 9, 3) equal, (3, 9, 3) +0.6, (2, 9, 3) +1.1, (1, 9, 1) +1.6 us
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
 static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 
-enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7 };
+enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7, kCfgB9 = 8 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) of one weight type and layout over upr units per row.

@@ -323,7 +323,7 @@ def test_balanced_tiling_edges(m27q, ora, dev, type_name, rc, k, layout):
 
 @pytest.mark.parametrize("layout_name", ["TILED", "GGUF"])
 @pytest.mark.parametrize("type_name", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
-@pytest.mark.parametrize("rc,units", [(4098, 24), (5117, 2), (5120, 68), (1030, 9)])
+@pytest.mark.parametrize("rc,units", [(4098, 24), (5117, 2), (5120, 68), (1030, 9), (17001, 20)])
 def test_single_product_edges_every_type(m27q, ora, dev, layout_name, type_name, rc, units):
     """Single products around the balanced-tiling rule, every integer-dot type
     and both layouts: 513 tiles with a last tile of 2 rows (24 units), 640
@@ -331,7 +331,9 @@ def test_single_product_edges_every_type(m27q, ora, dev, layout_name, type_name,
     K slices: waves with nothing to stream), the 68-unit down shape (balanced
     tiling on quantized input), and rows of an odd unit count (GGUF Q6_K: every
     other row starts 2 bytes past a multiple of 4; one-tile waves read its
-    fields as shifted dwords).  The quantized-input and the fp32-input
+    fields as shifted dwords), and 2126 tiles with a last tile of one row
+    (8-9 tiles per CU: balanced tiling with up to 9 tiles per workgroup,
+    three per wave).  The quantized-input and the fp32-input
     products, each with a residual, against the integer-dot oracle (in-kernel
     quantization gives the same codes), the rows past row_count untouched."""
     import torch
