@@ -40,7 +40,9 @@
 // zero operand lanes read a zero record.  K is split over the KS waves of a
 // workgroup, one row set per workgroup, and the KS partials are added in LDS
 // in a fixed order.  Padding tokens (past M) read a real token's codes; their
-// scales are zero and their outputs are dropped.
+// scales are zero and their outputs are dropped.  GGUF-layout Q4_K / Q5_K /
+// Q6_K weights fill the same LDS records from each row's block of the unit
+// (k_matmul_mfma's LAYOUT parameter).
 //
 // No reference counterpart: the reference runs prefill and decode one token at
 // a time (src/mono27b_chat.cpp:399-403).
