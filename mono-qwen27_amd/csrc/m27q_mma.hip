@@ -529,13 +529,11 @@ struct Stage {
 // back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
 // Waves per SIMD the register budget is cut for, the most that compiles
-// without spills: one-set launches 4 (128 VGPRs; Q4_K gate/up at M = 16 runs
-// 2 us faster than at 3), two-set launches 3; Q5_K and Q6_K one less (their
-// two-set launches have 160 row sets for 256 CUs at the model's shapes, so
-// the lower occupancy costs nothing).
-template <class T, int PK>
+// without spills (128 VGPRs for 4): 4, but 3 for the two-set Q5_K and Q6_K
+// kernels and for GGUF-layout Q5_K / Q6_K.
+template <class T, int PK, int LAYOUT>
 constexpr int mm_waves_per_eu() {
-    return (PK == 2 ? 3 : 4) - (T::kWide ? 1 : 0);
+    return T::kWide && (PK == 2 || LAYOUT == M27Q_LAYOUT_GGUF) ? 3 : 4;
 }
 // GGUF-layout weights (LAYOUT == M27Q_LAYOUT_GGUF; Q4_K, Q5_K and Q6_K): the
 // same LDS records, staged from each row's block of the unit (row_blocks ==
@@ -554,7 +552,8 @@ __device__ __forceinline__ v4u shift16(const v4u &v, uint32_t e, uint32_t sh) {
 }
 
 template <class T, int PK, int KS, int LAYOUT>
-__global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmul_mfma(MatmulMultiParams p, int m0) {
+__global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void k_matmul_mfma(MatmulMultiParams p,
+                                                                                            int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     using SG = Stage<T, PK>;
     constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;
@@ -719,17 +718,25 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK>())) void k_matmu
 
     float acc[4] = {0.f, 0.f, 0.f, 0.f}, u4[4] = {0.f, 0.f, 0.f, 0.f};
     v4f cm = v4f{0.f, 0.f, 0.f, 0.f};  // Q4_K min term
+    // One half unit at a time: its operands are read from LDS just before
+    // its MFMAs, so only one half's fragments are live (the two-set Q4_K
+    // kernel 129 VGPRs against 155 with both halves read first).
     auto compute = [&]() __attribute__((always_inline)) {
-        typename T::template Frag<PK> f0, f1;
-        AFrag<NP> x0, x1;
-        T::template load<PK>(f0, wl, wrow, L.r, 0, SG::kSide);
-        load_act<NP>(x0, ab, 0);
+        {
+            typename T::template Frag<PK> f0;
+            AFrag<NP> x0;
+            T::template load<PK>(f0, wl, wrow, L.r, 0, SG::kSide);
+            load_act<NP>(x0, ab, 0);
+            compute_half<T, PK, 0>(f0, x0, sl, 0, L, areal, atok, acc, u4, cm);
+        }
         if constexpr (NS == 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            typename T::template Frag<PK> f1;
+            AFrag<NP> x1;
             T::template load<PK>(f1, wl, wrow, L.r, 1, SG::kSide);
             load_act<NP>(x1, ab, 1);
+            compute_half<T, PK, 1>(f1, x1, sl, 0, L, areal, atok, acc, u4, cm);
         }
-        compute_half<T, PK, 0>(f0, x0, sl, 0, L, areal, atok, acc, u4, cm);
-        if constexpr (NS == 2) compute_half<T, PK, 1>(f1, x1, sl, 0, L, areal, atok, acc, u4, cm);
     };
     // Loads are unconditional inside the loop (a conditional reload makes the
     // compiler wait for every load before each use); the last unit is peeled.
