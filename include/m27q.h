@@ -251,11 +251,11 @@ M27Q_API m27q_status m27q_matvec_f32(const m27q_weight *w, const float *x, float
 /* Y[m][r] = sum_k W[r][k] * xq[m][k] (+ residual[m][r]) for m < M, 1 <= M <= 64,
  * xq from m27q_quant_act with this M (the whole buffer of m27q_act_bytes(M,
  * K) bytes: Q8_0 weights whose K is not a multiple of 128 read up to 96 bytes
- * past the last row's codes); Y is [M][row_count].  TILED weights run on the
- * GEMV structure for M = 2 and on int8 MFMA (v_mfma_i32_16x16x32_i8, up to 16
- * activation rows per launch) from M = 3; GGUF-layout Q4_K / Q5_K / Q6_K
- * weights on int8 MFMA from M = 2, other GGUF-layout weights on a
- * packed-int8-dot path; M = 1 is m27q_matvec_q8.  No reference
+ * past the last row's codes); Y is [M][row_count].  M = 2 runs on the GEMV
+ * structure, from M = 3 TILED weights and GGUF-layout Q4_K / Q5_K / Q6_K
+ * weights on int8 MFMA (v_mfma_i32_16x16x32_i8, up to 16 activation rows per
+ * launch), other GGUF-layout weights on a packed-int8-dot path; M = 1 is
+ * m27q_matvec_q8.  No reference
  * counterpart: the reference runs prefill and decode one token at a time
  * (src/mono27b_chat.cpp:399-403); results equal M independent M = 1 products
  * up to fp32 rounding. */

@@ -206,9 +206,10 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
 // (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).  Measured on the
 // Qwen-27B layer: 56 us against 63 at M = 2; from M = 3 on the MFMA kernel
 // with two row sets per tile is faster (63 against 75 us at M = 4).
-// GGUF-layout Q4_K / Q5_K / Q6_K weights take the MFMA kernel from M = 2 on
-// (staged from the row blocks); GGUF-layout Q8_0 and IQ4_XS weights, one
-// launch per matrix of the VALU kernel (m27q_matmul.hip).
+// GGUF-layout weights take the same few-token kernel (with temporal loads);
+// from M = 3, GGUF-layout Q4_K / Q5_K / Q6_K take the MFMA kernel (staged from
+// the row blocks), GGUF-layout Q8_0 and IQ4_XS one launch per matrix of the
+// VALU kernel (m27q_matmul.hip).
 constexpr int kMtMaxM = 2;
 constexpr size_t kMtLdsBudget = 80 * 1024;  // two workgroups per CU
 
@@ -228,10 +229,12 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     const bool tiled = layout == M27Q_LAYOUT_TILED;
     MatmulMultiParams p{};
     p.upr = units_per_row(type, ws[0].row_blocks);
+    p.rb = (int)ws[0].row_blocks;
     p.K = k_of(&ws[0]);
     p.M = M;
     const ActView a = act_view(xq, M, p.K);
-    if (!matmul_mfma_takes(type, layout)) {  // GGUF Q8_0 / IQ4_XS
+    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(type, p.upr) <= kMtLdsBudget;
+    if (!few && !matmul_mfma_takes(type, layout)) {  // GGUF Q8_0 / IQ4_XS from M = 3
         if (dry) return M27Q_OK;
         for (int i = 0; i < n; ++i) {
             MatmulParams q{};
@@ -251,7 +254,6 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
         }
         return M27Q_OK;
     }
-    const bool few = tiled && M <= kMtMaxM && matmul_mt_lds_bytes(type, p.upr) <= kMtLdsBudget;
     if (!few && matmul_mfma_lds_bytes(type) > lds_limit()) return M27Q_ERR_SHAPE;
     // The MFMA kernel reads each matrix through a buffer descriptor with a
     // 32-bit size; the activations (M <= kMaxM rows of K <= kMaxK) stay far
@@ -273,7 +275,7 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
         p.res[i] = res[i];
         p.rc[i] = (int)ws[i].row_count;
     }
-    return hip_status(few ? launch_matmul_mt(type, p, stream) : launch_matmul_mfma(type, layout, p, stream));
+    return hip_status(few ? launch_matmul_mt(type, layout, p, stream) : launch_matmul_mfma(type, layout, p, stream));
 }
 
 // Up to kMaxMulti weights of one K sharing one activation, of any mix of

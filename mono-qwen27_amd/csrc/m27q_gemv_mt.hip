@@ -1,9 +1,10 @@
 // m27q_gemv_mt.hip -- small-M products Y[M][N] = X[M][K] W[N][K]^T for a few
 // tokens on the M = 1 GEMV's streaming structure.
 //
-// The weights are streamed exactly as by the M = 1 kernel (TILED layout, 8-row
-// tiles, K split over KS waves, 16-byte loads of one unit per lane, double
-// buffered and unconditional), and every loaded fragment is applied to MT
+// The weights are streamed exactly as by the M = 1 kernel (8-row tiles, K
+// split over KS waves, 16-byte loads of one unit per lane, double buffered and
+// unconditional; TILED or, with temporal loads, GGUF layout), and every
+// loaded fragment is applied to MT
 // activation rows staged in LDS: the weight unpacking is shared by the tokens,
 // each token adds its own integer dots and scale terms, and no lane works on a
 // padding token unless M is not a multiple of MT.  Its cost grows with the
@@ -18,7 +19,7 @@
 
 namespace m27q {
 
-template <class T, class C, int MT>
+template <class T, class C, int MT, int LAYOUT>
 __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
@@ -50,7 +51,9 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
 
     // First unit of weights before the staging, so their latencies overlap.
     const uint8_t *W[1] = {p.W[mi]};
-    const UnitStream<T, M27Q_LAYOUT_TILED, 1, WT, C::NT> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt), rc, 0, p.upr, lane);
+    // GGUF layout: temporal loads (a row's consecutive blocks share lines)
+    const UnitStream<T, LAYOUT, 1, WT, C::NT && LAYOUT == M27Q_LAYOUT_TILED> ws(W, tile0 + tg * WT, min(ntiles, tile0 + nt),
+                                                                               rc, p.rb, p.upr, lane);
     typename T::Frag fa[1][WT], fb[1][WT];
     ws.load(fa, min(ub, p.upr - 1));
 
@@ -173,7 +176,7 @@ static size_t mt_lds(int upr) {
     return MT * (Kp + Kp / 8 * (1 + T::kAuxWords)) + (size_t)MT * C::KS * C::TPW * kTileRows * sizeof(float);
 }
 
-template <class T, class C, int MT>
+template <class T, class C, int MT, int LAYOUT>
 static hipError_t launch_mt_cfg(MatmulMultiParams p, hipStream_t s) {
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
@@ -183,7 +186,7 @@ static hipError_t launch_mt_cfg(MatmulMultiParams p, hipStream_t s) {
     p.wg_start[p.nmat] = total;
     const size_t lds = mt_lds<T, C, MT>(p.upr);
     for (int m0 = 0; m0 < p.M; m0 += MT) {
-        hipLaunchKernelGGL((k_gemv_mt<T, C, MT>), dim3(total), dim3(kWave * C::NW), lds, s, p, m0);
+        hipLaunchKernelGGL((k_gemv_mt<T, C, MT, LAYOUT>), dim3(total), dim3(kWave * C::NW), lds, s, p, m0);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -207,18 +210,24 @@ int matmul_mt_balance(long long tiles, int upr, int cus) {
     return upr < 40 && tiles > 2LL * cus && tiles <= (long long)CfgB::TPW * cus ? cus : 0;
 }
 
-template <class T, int MT>
+template <class T, int MT, int LAYOUT>
 static hipError_t launch_mt_t(const MatmulMultiParams &p, hipStream_t s) {
-    if (p.bal_wgs > 0) return launch_mt_cfg<T, CfgB, MT>(p, s);
+    if (p.bal_wgs > 0) return launch_mt_cfg<T, CfgB, MT, LAYOUT>(p, s);
     long long rows = 0;
     for (int i = 0; i < p.nmat; ++i) rows += p.rc[i];
     const int cfg = pick_mt_cfg(rows, p.upr);
     switch (cfg) {
-        case kCfg81: return launch_mt_cfg<T, Cfg81, MT>(p, s);
-        case kCfg42: return launch_mt_cfg<T, Cfg42, MT>(p, s);
-        case kCfg84: return launch_mt_cfg<T, Cfg84, MT>(p, s);
-        default: return launch_mt_cfg<T, Cfg41, MT>(p, s);
+        case kCfg81: return launch_mt_cfg<T, Cfg81, MT, LAYOUT>(p, s);
+        case kCfg42: return launch_mt_cfg<T, Cfg42, MT, LAYOUT>(p, s);
+        case kCfg84: return launch_mt_cfg<T, Cfg84, MT, LAYOUT>(p, s);
+        default: return launch_mt_cfg<T, Cfg41, MT, LAYOUT>(p, s);
     }
+}
+
+template <class T, int MT>
+static hipError_t launch_mt_l(const MatmulMultiParams &p, int layout, hipStream_t s) {
+    return layout == M27Q_LAYOUT_TILED ? launch_mt_t<T, MT, M27Q_LAYOUT_TILED>(p, s)
+                                       : launch_mt_t<T, MT, M27Q_LAYOUT_GGUF>(p, s);
 }
 
 size_t matmul_mt_lds_bytes(uint32_t type, int upr) {
@@ -239,13 +248,13 @@ size_t matmul_mt_lds_bytes(uint32_t type, int upr) {
 }
 
 // Two tokens per launch.
-hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s) {
+hipError_t launch_matmul_mt(uint32_t type, int layout, const MatmulMultiParams &p, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_mt_t<Q4K, 2>(p, s);
-        case kQ5_K: return launch_mt_t<Q5K, 2>(p, s);
-        case kQ6_K: return launch_mt_t<Q6K, 2>(p, s);
-        case kQ8_0: return launch_mt_t<Q80, 2>(p, s);
-        case kIQ4_XS: return launch_mt_t<IQ4XS, 2>(p, s);
+        case kQ4_K: return launch_mt_l<Q4K, 2>(p, layout, s);
+        case kQ5_K: return launch_mt_l<Q5K, 2>(p, layout, s);
+        case kQ6_K: return launch_mt_l<Q6K, 2>(p, layout, s);
+        case kQ8_0: return launch_mt_l<Q80, 2>(p, layout, s);
+        case kIQ4_XS: return launch_mt_l<IQ4XS, 2>(p, layout, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -93,6 +93,7 @@ struct MatmulMultiParams {
     int wg_start[kMaxMulti + 1];
     int nmat;
     int upr, K, M;
+    int rb;  // GGUF blocks per row (the few-token kernel's GGUF rows)
     const int8_t *xq;
     const float *xd;
     const uint32_t *xs;
@@ -102,12 +103,12 @@ struct MatmulMultiParams {
 };
 hipError_t launch_matmul_q8(uint32_t type, int layout, const MatmulParams &p, hipStream_t s);
 // Few-token products on the GEMV streaming structure (m27q_gemv_mt.hip): two
-// activation rows, TILED weights.  matmul_mt_balance(): the balanced
+// activation rows, either layout.  matmul_mt_balance(): the balanced
 // workgroup count for one matrix of `tiles` tiles of `upr` units on `cus`
 // CUs, or 0.
 size_t matmul_mt_lds_bytes(uint32_t type, int upr);
 int matmul_mt_balance(long long tiles, int upr, int cus);
-hipError_t launch_matmul_mt(uint32_t type, const MatmulMultiParams &p, hipStream_t s);
+hipError_t launch_matmul_mt(uint32_t type, int layout, const MatmulMultiParams &p, hipStream_t s);
 // int8-MFMA small-M products (m27q_mma.hip): TILED weights of every type and
 // GGUF-layout Q4_K / Q5_K / Q6_K (matmul_mfma_takes), any M (16 tokens per
 // launch).

@@ -55,6 +55,9 @@ CASES = [  # type, rows, K, M, layout
     ("Q5_K", 6144, 5120, 2, 0), ("Q5_K", 8200, 512, 8, 0), ("Q5_K", 16390, 1024, 25, 0),
     ("Q6_K", 24, 768, 2, 0), ("Q6_K", 8200, 768, 7, 0), ("Q6_K", 16390, 1024, 16, 0), ("Q6_K", 1030, 2304, 11, 0),
     ("Q6_K", 5120, 17408, 16, 0), ("Q6_K", 33, 2304, 4, 0),
+    # GGUF-layout weights at M = 2 on the few-token kernel: o's shape (balanced
+    # over one workgroup per CU), IQ4_XS and Q8_0 (its 34-byte blocks)
+    ("Q4_K", 5120, 6144, 2, 0), ("IQ4_XS", 40, 512, 2, 0), ("Q8_0", 13, 160, 2, 0),
 ]
 
 
