@@ -38,8 +38,9 @@
 // its own LDS area (padded row and token records, so the operand reads below
 // are free of bank conflicts), and reads the MFMA operands from there.  The
 // zero operand lanes read a zero record.  K is split over the KS waves of a
-// workgroup, one row set per workgroup, and the KS partials are added in LDS
-// in a fixed order.  Padding tokens (past M) read a real token's codes; their
+// workgroup, one row set per workgroup (two for one-set tiles, sharing the
+// activation operands), and the KS partials are added in LDS in a fixed
+// order.  Padding tokens (past M) read a real token's codes; their
 // scales are zero and their outputs are dropped.  GGUF-layout Q4_K / Q5_K /
 // Q6_K weights fill the same LDS records from each row's block of the unit
 // (k_matmul_mfma's LAYOUT parameter).
@@ -491,7 +492,8 @@ __device__ __forceinline__ void compute_half(const typename T::template Frag<PK>
 }
 
 // Per-wave LDS staging area for one unit (bytes):
-//   W: 16 PK row records of T::kRowBytes, then a side area (64 bytes per tile)
+//   W: 16 PK RS row records of T::kRowBytes (RS row sets per workgroup), then
+//      a side area (64 bytes per tile)
 //   A: TK token records of 32 G + 16 bytes (G groups of codes + pad), then,
 //      for PK = 2 (and Q6_K's zero-split views), one record of zeros for the
 //      operand lanes of the other set (or sub-block)
@@ -500,11 +502,11 @@ __device__ __forceinline__ void compute_half(const typename T::template Frag<PK>
 // The paddings keep the MFMA-layout reads free of bank conflicts: the row
 // strides 144, 176, 240 and the token strides 272, 144 put the 16 rows (or
 // tokens) of a half wave on distinct 4-bank groups.
-template <class T, int PK>
+template <class T, int PK, int RS = 1>
 struct Stage {
     static constexpr int G = T::kGroups, TK = Pack<PK>::TK, UE = 32 * G, UB = T::kUnitBytes;
-    static constexpr int kSide = 16 * PK * T::kRowBytes;
-    static constexpr int kW = kSide + 2 * PK * 64;
+    static constexpr int kSide = 16 * PK * RS * T::kRowBytes;
+    static constexpr int kW = kSide + 2 * PK * RS * 64;
     static constexpr int kARow = UE + 16;
     static constexpr int oA = kW;
     static constexpr int oZero = oA + TK * kARow;
@@ -512,7 +514,7 @@ struct Stage {
     static constexpr int oS = oZero + (kZeroRec ? UE : 0);
     static constexpr int oDummy = oS + G * TK * 4 * (T::kAux ? 2 : 1);
     static constexpr int kBytes = (oDummy + 16 + 15) / 16 * 16;
-    static constexpr int kWChunks = 2 * PK * UB / 16;  // 16-byte chunks of the set's unit
+    static constexpr int kWChunks = 2 * PK * RS * UB / 16;  // 16-byte chunks of the sets' unit
     static constexpr int kNW = (kWChunks + kWave - 1) / kWave;
     static constexpr int kAChunks = TK * UE / 16;
     static constexpr int kNA = (kAChunks + kWave - 1) / kWave;
@@ -522,18 +524,19 @@ struct Stage {
     static_assert(UB % 16 == 0 && kARow % 16 == 0 && T::kRowBytes % 16 == 0, "16-byte staging");
 };
 
-// One workgroup: one row set of 16 PK rows of one matrix, K split over the KS
-// waves.  Each wave streams its K slice one unit at a time: 16-byte loads of
+// One workgroup: RS row sets of 16 PK rows of one matrix (RS = 2 only with
+// PK = 1), K split over the KS waves.  Each wave streams its K slice one unit at a time: 16-byte loads of
 // the unit's weight tiles, activation codes and scales into registers (issued
 // while the previous unit computes), written to the wave's LDS area, read
 // back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
 // Waves per SIMD the register budget is cut for, the most that compiles
 // without spills (128 VGPRs for 4): 4, but 3 for the two-set Q5_K and Q6_K
-// kernels and for GGUF-layout Q5_K / Q6_K.
-template <class T, int PK, int LAYOUT>
+// kernels, for GGUF-layout Q5_K / Q6_K and for Q4_K / Q5_K / Q6_K with two
+// row sets per workgroup.
+template <class T, int PK, int LAYOUT, int RS>
 constexpr int mm_waves_per_eu() {
-    return T::kWide && (PK == 2 || LAYOUT == M27Q_LAYOUT_GGUF) ? 3 : 4;
+    return (T::kWide || (RS == 2 && T::kAux)) && (PK == 2 || RS == 2 || LAYOUT == M27Q_LAYOUT_GGUF) ? 3 : 4;
 }
 // GGUF-layout weights (LAYOUT == M27Q_LAYOUT_GGUF; Q4_K, Q5_K and Q6_K): the
 // same LDS records, staged from each row's block of the unit (row_blocks ==
@@ -551,13 +554,15 @@ __device__ __forceinline__ v4u shift16(const v4u &v, uint32_t e, uint32_t sh) {
                __builtin_amdgcn_alignbit(v.w, v.z, sh), __builtin_amdgcn_alignbit(e, v.w, sh)};
 }
 
-template <class T, int PK, int KS, int LAYOUT>
-__global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void k_matmul_mfma(MatmulMultiParams p,
-                                                                                            int m0) {
+template <class T, int PK, int KS, int LAYOUT, int RS>
+__global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) void k_matmul_mfma(
+    MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
-    using SG = Stage<T, PK>;
+    using SG = Stage<T, PK, RS>;
     constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;
-    static_assert(!kG || 16 * PK * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
+    constexpr int SR = 16 * PK * RS;  // rows of the workgroup
+    static_assert(RS == 1 || PK == 1, "two row sets per workgroup only with one-set tiles");
+    static_assert(!kG || SR * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
     constexpr int G = T::kGroups, NS = T::kSteps, TK = Pack<PK>::TK, UE = SG::UE, UB = SG::UB;
     constexpr int CPU = UB / 16;  // chunks per tile unit
     const int lane = (int)(threadIdx.x & 63);
@@ -572,7 +577,7 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void
     const int Mloc = min(p.M - m0, TK);
     const int ngroups = p.K / 32;
     const int ntiles8 = (rc + kTileRows - 1) / kTileRows;
-    const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * 16 * PK;
+    const int row0 = ((int)blockIdx.x - p.wg_start[mi]) * SR;
     uint8_t *wl = smem + (size_t)wave * SG::kBytes;
 
     // This wave's K slice (units).
@@ -594,7 +599,7 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void
     for (int n = 0; n < SG::kNW; ++n) {
         const int id = n * kWave + lane;
         if constexpr (kG) {
-            const bool ok = id < 16 * PK * T::kGgufChunks;
+            const bool ok = id < SR * T::kGgufChunks;
             const int j = ok ? id / T::kGgufChunks : 0, c = ok ? id % T::kGgufChunks : 0;
             goff[n] = (uint32_t)min(row0 + j, rc - 1) * rowb + 16u * c;
             wdst[n] = ok ? T::gguf_dst(j, c) : SG::oDummy;
@@ -611,9 +616,9 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void
     // 256-byte aligned), and every offset carries the base's low bits, so
     // the dword reads and shifts follow the absolute addresses.
     const uint32_t blo = kG && T::kGgufA2 ? (uint32_t)((uintptr_t)Wm & 3u) : 0u;
-    // GGUF Q6_K: lanes 0 .. 16 PK - 1 stage the d of row `lane` of the set
-    const uint32_t doff = blo + (uint32_t)min(row0 + (lane & (16 * PK - 1)), rc - 1) * rowb + (uint32_t)kQ6KD;
-    const int ddst = lane < 16 * PK ? SG::kSide + 16 * (lane >> 3) + 2 * (lane & 7) : SG::oDummy;
+    // GGUF Q6_K: lanes 0 .. SR - 1 stage the d of row `lane` of the sets
+    const uint32_t doff = blo + (uint32_t)min(row0 + (lane & (SR - 1)), rc - 1) * rowb + (uint32_t)kQ6KD;
+    const int ddst = lane < SR ? SG::kSide + 16 * (lane >> 3) + 2 * (lane & 7) : SG::oDummy;
     uint32_t aoff[SG::kNA];
     int adst[SG::kNA];
 #pragma unroll
@@ -716,26 +721,35 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void
     }
     const ScaleLds<PK> sl{(const float *)(wl + SG::oS), (const float *)(wl + SG::oS) + G * TK};
 
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, u4[4] = {0.f, 0.f, 0.f, 0.f};
-    v4f cm = v4f{0.f, 0.f, 0.f, 0.f};  // Q4_K min term
+    float acc[RS][4], u4[RS][4];
+    v4f cm[RS];  // Q4_K min term
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        cm[r] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[r][e] = u4[r][e] = 0.f;
+    }
     // One half unit at a time: its operands are read from LDS just before
     // its MFMAs, so only one half's fragments are live (the two-set Q4_K
-    // kernel 129 VGPRs against 155 with both halves read first).
-    auto compute = [&]() __attribute__((always_inline)) {
-        {
-            typename T::template Frag<PK> f0;
-            AFrag<NP> x0;
-            T::template load<PK>(f0, wl, wrow, L.r, 0, SG::kSide);
-            load_act<NP>(x0, ab, 0);
-            compute_half<T, PK, 0>(f0, x0, sl, 0, L, areal, atok, acc, u4, cm);
+    // kernel 129 VGPRs against 155 with both halves read first).  With RS = 2
+    // the half's activation operands serve both row sets.
+    auto half = [&](auto st) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st)::value;
+        AFrag<NP> x;
+        load_act<NP>(x, ab, ST);
+#pragma unroll
+        for (int r = 0; r < RS; ++r) {
+            typename T::template Frag<PK> f;
+            T::template load<PK>(f, wl, wrow + 16 * r, L.r, ST, SG::kSide);
+            compute_half<T, PK, ST>(f, x, sl, 0, L, areal, atok, acc[r], u4[r], cm[r]);
+            if (r + 1 < RS) __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    auto compute = [&]() __attribute__((always_inline)) {
+        half(IntTag<0>{});
         if constexpr (NS == 2) {
             __builtin_amdgcn_sched_barrier(0);
-            typename T::template Frag<PK> f1;
-            AFrag<NP> x1;
-            T::template load<PK>(f1, wl, wrow, L.r, 1, SG::kSide);
-            load_act<NP>(x1, ab, 1);
-            compute_half<T, PK, 1>(f1, x1, sl, 0, L, areal, atok, acc, u4, cm);
+            half(IntTag<1>{});
         }
     };
     // Loads are unconditional inside the loop (a conditional reload makes the
@@ -754,23 +768,27 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT>())) void
     }
     if (T::kAux) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] -= cm[e];
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[r][e] -= cm[r][e];
     }
 
     // Partials of this wave's K slice -> LDS (over the staging areas), then
-    // one thread per (lane, e) adds the KS waves in a fixed order.
+    // one thread per (set, lane, e) adds the KS waves in a fixed order.
     __syncthreads();
-    float *red = (float *)smem;  // [KS][4][64]
+    float *red = (float *)smem;  // [KS][RS][4][64]
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[(wave * 4 + e) * kWave + lane] = acc[e];
+    for (int r = 0; r < RS; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[((wave * RS + r) * 4 + e) * kWave + lane] = acc[r][e];
     __syncthreads();
-    for (int idx = (int)threadIdx.x; idx < 4 * kWave; idx += KS * kWave) {
-        const int e = idx / kWave, ln = idx % kWave;
+    for (int idx = (int)threadIdx.x; idx < RS * 4 * kWave; idx += KS * kWave) {
+        const int r = idx / (4 * kWave), e = idx / kWave % 4, ln = idx % kWave;
         float v = red[idx];
 #pragma unroll
-        for (int w = 1; w < KS; ++w) v += red[(w * 4 + e) * kWave + ln];
+        for (int w = 1; w < KS; ++w) v += red[((w * RS + r) * 4 + e) * kWave + ln];
         const Lane<PK> O(ln);
-        const int row = row0 + O.c + 16 * O.s, tok = 4 * O.r + e;
+        const int row = row0 + 16 * r + O.c + 16 * O.s, tok = 4 * O.r + e;
         if (row < rc && tok < Mloc) {
             const size_t o = (size_t)(m0 + tok) * rc + row;
             p.Y[mi][o] = v + (p.res[mi] ? p.res[mi][o] : 0.f);
@@ -1043,21 +1061,22 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
     }
 }
 
-template <class T, int PK, int KS>
+template <class T, int PK, int KS, int RS = 1>
 static size_t mfma_lds() {
-    return (size_t)KS * Stage<T, PK>::kBytes;
+    return (size_t)KS * Stage<T, PK, RS>::kBytes;
 }
 
-template <class T, int PK, int KS, int LAYOUT>
+template <class T, int PK, int KS, int LAYOUT, int RS>
 static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
-    const size_t lds = mfma_lds<T, PK, KS>();
+    const size_t lds = mfma_lds<T, PK, KS, RS>();
+    constexpr int SR = 16 * PK * RS;
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
         p.wg_start[i] = total;
-        total += (p.rc[i] + 16 * PK - 1) / (16 * PK);
+        total += (p.rc[i] + SR - 1) / SR;
     }
     p.wg_start[p.nmat] = total;
-    hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS, LAYOUT>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
+    hipLaunchKernelGGL((k_matmul_mfma<T, PK, KS, LAYOUT, RS>), dim3(total), dim3(kWave * KS), lds, s, p, m0);
     return hipGetLastError();
 }
 
@@ -1101,21 +1120,28 @@ static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipEr
     else return launch_xres_t<T, LAYOUT>(p, m0, s, err);
 }
 
-// Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 16: a
-// launch of fewer than 320 row sets (q/k/v, o and down with two-set tiles)
-// splits K over 8 waves, a larger one over 4; more waves per set cost more
-// than they hide.  One-set tiles (M > 8) on K <= 6144 (q/k/v, gate/up, o)
-// also split over 8: at M = 16 gate/up 35.6 us against 37.7, q/k/v and o
-// 0.3 us faster; down (K = 17408) was 1.6 us slower so.  Two row sets per tile whenever at most 8 tokens are left
-// and the product has at least 128 sets of 32 rows (every product of the
-// layer): down at M = 8 takes 21.7 us against 28.8 with one-set tiles.
+// Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 12, 16: a
+// launch of fewer than 320 workgroups (q/k/v, o and down with two-set tiles
+// or two one-set tiles per workgroup) splits K over 8 waves, a larger one over
+// 4; more waves per set cost more than they hide.  Two row sets per tile
+// whenever at most 8 tokens are left and the product has at least 128 sets
+// of 32 rows (every product of the layer): down at M = 8 takes 21.7 us
+// against 28.8 with one-set tiles.  One-set tiles (more than 8 tokens left)
+// take two row sets per workgroup (RS = 2), each wave's activation operands
+// serving both: at M = 16 q/k/v 9.6 us against 10.4, o 10.1 against 11.5,
+// down 27.4 against 28.2; gate/up at M = 12 30.1 against 32.0.  GGUF-layout
+// Q6_K keeps one set per workgroup (its shifted chunk loads do not fit the
+// registers of two).  One set per workgroup splits K over 8 waves also on
+// K <= 6144 (at M = 16 gate/up 35.6 us against 37.7).
 constexpr int kPk2MinSets = 128;
 template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
-    long long sets = 0;
-    for (int i = 0; i < p.nmat; ++i) sets += (p.rc[i] + 16 * PK - 1) / (16 * PK);
-    const int ks = (sets < 320 || (PK == 1 && p.K <= 6144)) ? 8 : 4;
-    return ks == 8 ? launch_mfma_t<T, PK, 8, LAYOUT>(p, m0, s) : launch_mfma_t<T, PK, 4, LAYOUT>(p, m0, s);
+    constexpr int RS = PK == 1 && !(LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) ? 2 : 1;
+    constexpr int SR = 16 * PK * RS;
+    long long wgs = 0;
+    for (int i = 0; i < p.nmat; ++i) wgs += (p.rc[i] + SR - 1) / SR;
+    const int ks = (wgs < 320 || (PK == 1 && RS == 1 && p.K <= 6144)) ? 8 : 4;
+    return ks == 8 ? launch_mfma_t<T, PK, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, PK, 4, LAYOUT, RS>(p, m0, s);
 }
 
 template <class T, int LAYOUT>
@@ -1138,7 +1164,7 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
 
 template <class T>
 static size_t mfma_lds_max() {
-    return std::max(mfma_lds<T, 1, 8>(), mfma_lds<T, 2, 8>());
+    return std::max({mfma_lds<T, 1, 8>(), mfma_lds<T, 2, 8>(), mfma_lds<T, 1, 8, 2>()});
 }
 
 size_t matmul_mfma_lds_bytes(uint32_t type) {
