@@ -22,7 +22,8 @@
 // quarter q = lane / 16, column c = lane % 16, NQ = 4 / PK quarters per row
 // set, set s = q / NQ, piece lane r = q % NQ:
 //   B (weights):     lane holds row c + 16 s, the 8 positions 8 r + (32/PK) m
-//                    of the group for MFMA m;
+//                    of the group for MFMA m (Q4_K, Q5_K and Q8_0 at PK = 2:
+//                    16 r + 8 m, see kPaired);
 //   A (activations): lane holds token c % (16/PK) at the same positions, or
 //                    zeros if c / (16/PK) != s;
 //   C:               lane holds tokens 4 r .. 4 r + 3 of row c + 16 s.
@@ -125,6 +126,22 @@ __device__ __forceinline__ void load_act(AFrag<NP> &f, const uint8_t *const (&ba
         for (int m = 0; m < NP; ++m) f.a[jg][m] = ld8(base[m] + 32 * (4 * st + jg));
 }
 
+// Paired pieces (a policy's kPaired at PK = 2): the lane's two pieces of a
+// group are the adjacent positions 16 r .. 16 r + 15, read as one 16-byte LDS
+// load.  Two 8-byte pieces 16 bytes apart issue as ds_read2_b64, which the
+// LDS serves at half the rate of ds_read_b128 (measured on gfx950: 8 against
+// 4 bank-conflict cycles per instruction for the same kilobyte).  The split
+// of a group's 32 positions over lanes and MFMAs is free where one scale
+// covers the group, as long as both operands follow it.
+__device__ __forceinline__ void load_act_paired(AFrag<2> &f, const uint8_t *base, int st) {
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+        const uint4 v = *(const uint4 *)(base + 32 * (4 * st + jg));
+        f.a[jg][0] = make_uint2(v.x, v.y);
+        f.a[jg][1] = make_uint2(v.z, v.w);
+    }
+}
+
 // ------------------------------------------------------------ Q4_K, Q5_K --
 // Q5_K is Q4_K with a fifth code bit per weight: bit j of qh[l] for position l
 // of group j (exec:953-969), added to the operand bytes as 16.
@@ -134,6 +151,7 @@ struct MmQ4KT {
     static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
     static constexpr bool kWide = Q5;  // more live registers than 3 waves per SIMD allow at PK = 2
+    static constexpr bool kPaired = true;
     template <int PK>
     static constexpr int kPieces = PK;
     // The min term's token factor: dx * (sum of the 32 codes).
@@ -164,16 +182,27 @@ struct MmQ4KT {
     }
     template <int PK>
     __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int st, int) {
-        constexpr int W8 = Pack<PK>::W8;
         const uint8_t *rb = wl + row * kRowBytes;
+        if constexpr (PK == 2) {  // paired pieces: bytes 16 r .. 16 r + 15
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
+            for (int cc = 0; cc < 2; ++cc) {
+                const uint4 v = *(const uint4 *)(rb + 16 + 64 * st + 32 * cc + 16 * r);
+                f.qs[cc][0] = make_uint2(v.x, v.y);
+                f.qs[cc][1] = make_uint2(v.z, v.w);
+            }
+        } else {
 #pragma unroll
-            for (int m = 0; m < PK; ++m) f.qs[cc][m] = ld8(rb + 16 + 64 * st + 32 * cc + 8 * r + W8 * m);
+            for (int cc = 0; cc < 2; ++cc) f.qs[cc][0] = ld8(rb + 16 + 64 * st + 32 * cc + 8 * r);
+        }
         f.h = *(const uint4 *)rb;
         if constexpr (Q5) {
-#pragma unroll
-            for (int m = 0; m < PK; ++m) f.qh[m] = ld8(rb + 144 + 8 * r + W8 * m);
+            if constexpr (PK == 2) {
+                const uint4 v = *(const uint4 *)(rb + 144 + 16 * r);
+                f.qh[0] = make_uint2(v.x, v.y);
+                f.qh[1] = make_uint2(v.z, v.w);
+            } else {
+                f.qh[0] = ld8(rb + 144 + 8 * r);
+            }
         }
     }
     template <int PK, int ST>
@@ -241,6 +270,7 @@ struct MmQ6K {
     template <int PK>
     static constexpr int kPieces = 2;
     static constexpr bool kWide = true;
+    static constexpr bool kPaired = false;  // MFMA m is sub-block m (its own scale)
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     template <int PK>
     struct Frag {
@@ -341,6 +371,7 @@ struct MmQ80 {
     static constexpr int kUnitBytes = kQ80Unit;
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
+    static constexpr bool kPaired = true;
     // TILED only (34-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
     static constexpr int kBlockBytes = kQ80Bytes, kGgufChunks = 0;
     static constexpr bool kGgufA2 = false;
@@ -364,9 +395,15 @@ struct MmQ80 {
     __device__ static void load(Frag<PK> &f, const uint8_t *wl, int row, int r, int, int side) {
         const uint8_t *rb = wl + row * kRowBytes;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int m = 0; m < PK; ++m) f.qs[k][m] = ld8(rb + 32 * k + 8 * r + Pack<PK>::W8 * m);
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (PK == 2) {  // paired pieces
+                const uint4 v = *(const uint4 *)(rb + 32 * k + 16 * r);
+                f.qs[k][0] = make_uint2(v.x, v.y);
+                f.qs[k][1] = make_uint2(v.z, v.w);
+            } else {
+                f.qs[k][0] = ld8(rb + 32 * k + 8 * r);
+            }
+        }
         f.d = ld8(wl + side + 64 * (row >> 3) + 8 * (row & 7));
     }
     template <int PK, int ST>
@@ -399,6 +436,7 @@ struct MmIQ4XS {
     static constexpr int kUnitBytes = kIQ4XSUnit;
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
+    static constexpr bool kPaired = false;  // a piece is one nibble of 8 bytes
     // TILED only (136-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
     static constexpr int kBlockBytes = kIQ4XSBytes, kGgufChunks = 0;
     static constexpr bool kGgufA2 = false;
@@ -704,7 +742,8 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     const int wrow = L.c + 16 * L.s;
     const bool areal = L.c / TK == L.s;
     const int atok = L.c % TK;
-    const uint8_t *ar = wl + (areal ? SG::oA + atok * SG::kARow : SG::oZero) + 8 * L.r;
+    constexpr bool kPair = PK == 2 && T::kPaired;  // paired pieces: positions 16 r + 8 m
+    const uint8_t *ar = wl + (areal ? SG::oA + atok * SG::kARow : SG::oZero) + (kPair ? 16 : 8) * L.r;
     constexpr int NP = T::template kPieces<PK>;
     const uint8_t *ab[NP];
     if constexpr (NP == PK) {
@@ -736,7 +775,10 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     auto half = [&](auto st) __attribute__((always_inline)) {
         constexpr int ST = decltype(st)::value;
         AFrag<NP> x;
-        load_act<NP>(x, ab, ST);
+        if constexpr (kPair)
+            load_act_paired(x, ar, ST);
+        else
+            load_act<NP>(x, ab, ST);
 #pragma unroll
         for (int r = 0; r < RS; ++r) {
             typename T::template Frag<PK> f;
