@@ -45,12 +45,12 @@ def weight(m27q, ora, dev, t, rc, k, layout, seed, raw=False):
     return tid, wb, rb, m27q.Weight.upload(wb.reshape(-1), tid, rb, rc, layout, dev)
 
 
-@pytest.mark.parametrize("seed", range(64))
+@pytest.mark.parametrize("seed", range(256))
 def test_random_product_vs_oracle(m27q, ora, dev, seed):
     run_case(m27q, ora, dev, seed, raw=False)
 
 
-@pytest.mark.parametrize("seed", range(5000, 5032))
+@pytest.mark.parametrize("seed", range(5000, 5096))
 def test_random_bytes_vs_oracle(m27q, ora, dev, seed):
     run_case(m27q, ora, dev, seed, raw=True)
 
