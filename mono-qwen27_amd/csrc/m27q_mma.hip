@@ -150,7 +150,7 @@ struct MmQ4KT {
     static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
-    static constexpr bool kWide = Q5;  // more live registers than 3 waves per SIMD allow at PK = 2
+    static constexpr bool kWide = Q5;  // more live registers than 4 waves per SIMD allow at PK = 2 and in GGUF layout
     static constexpr bool kPaired = true;
     template <int PK>
     static constexpr int kPieces = PK;
