@@ -150,7 +150,8 @@ struct MmQ4KT {
     static constexpr int kGroups = 8, kSteps = 2;
     static constexpr int kUnitBytes = Q5 ? kQ5KUnit : kQ4KUnit;
     static constexpr bool kAux = true;
-    static constexpr bool kWide = Q5;  // more live registers than 4 waves per SIMD allow at PK = 2 and in GGUF layout
+    // more live registers than 4 waves per SIMD allow at PK = 2 and in GGUF layout
+    static constexpr bool kWide = Q5;
     static constexpr bool kPaired = true;
     template <int PK>
     static constexpr int kPieces = PK;
@@ -563,10 +564,10 @@ struct Stage {
 };
 
 // One workgroup: RS row sets of 16 PK rows of one matrix (RS = 2 only with
-// PK = 1), K split over the KS waves.  Each wave streams its K slice one unit at a time: 16-byte loads of
-// the unit's weight tiles, activation codes and scales into registers (issued
-// while the previous unit computes), written to the wave's LDS area, read
-// back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
+// PK = 1), K split over the KS waves.  Each wave streams its K slice one unit
+// at a time: 16-byte loads of the unit's weight tiles, activation codes and
+// scales into registers (issued while the previous unit computes), written to
+// the wave's LDS area, read back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
 // launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
 // Waves per SIMD the register budget is cut for, the most that compiles
 // without spills (128 VGPRs for 4): 4, but 3 for the two-set Q5_K and Q6_K
