@@ -1163,10 +1163,12 @@ static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipEr
     else return launch_xres_t<T, LAYOUT>(p, m0, s, err);
 }
 
-// Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 12, 16: a
-// launch of fewer than 320 workgroups (q/k/v, o and down with two-set tiles
-// or two one-set tiles per workgroup) splits K over 8 waves, a larger one over
-// 4; more waves per set cost more than they hide.  Two row sets per tile
+// Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 12, 16:
+// two-set tiles split K over 8 waves (gate/up's 1088 workgroups at M = 4 / 8:
+// 22.4 / 23.1 us against 23.3 / 23.7 with 4 waves, since the paired operand
+// reads; q/k/v, o and down took 8 already); one-set tiles over 8 waves in a
+// launch of fewer than 320 workgroups, else 4 (more waves per set cost more
+// than they hide there).  Two row sets per tile
 // whenever at most 8 tokens are left and the product has at least 128 sets
 // of 32 rows (every product of the layer): down at M = 8 takes 21.7 us
 // against 28.8 with one-set tiles.  One-set tiles (more than 8 tokens left)
@@ -1183,8 +1185,12 @@ static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t
     constexpr int SR = 16 * PK * RS;
     long long wgs = 0;
     for (int i = 0; i < p.nmat; ++i) wgs += (p.rc[i] + SR - 1) / SR;
-    const int ks = (wgs < 320 || (PK == 1 && RS == 1 && p.K <= 6144)) ? 8 : 4;
-    return ks == 8 ? launch_mfma_t<T, PK, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, PK, 4, LAYOUT, RS>(p, m0, s);
+    if constexpr (PK == 2) {
+        return launch_mfma_t<T, 2, 8, LAYOUT, RS>(p, m0, s);
+    } else {
+        const int ks = (wgs < 320 || (RS == 1 && p.K <= 6144)) ? 8 : 4;
+        return ks == 8 ? launch_mfma_t<T, 1, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, 1, 4, LAYOUT, RS>(p, m0, s);
+    }
 }
 
 template <class T, int LAYOUT>
