@@ -567,14 +567,18 @@ struct Stage {
 // PK = 1), K split over the KS waves.  Each wave streams its K slice one unit
 // at a time: 16-byte loads of the unit's weight tiles, activation codes and
 // scales into registers (issued while the previous unit computes), written to
-// the wave's LDS area, read back in the MFMA operand layout.  Up to kMaxMulti weights of one K share the
-// launch (workgroups [wg_start[i], wg_start[i+1]) serve i).
+// the wave's LDS area, read back in the MFMA operand layout.  Up to kMaxMulti
+// weights of one K share the launch (workgroups [wg_start[i], wg_start[i+1])
+// serve i).
 // Waves per SIMD the register budget is cut for, the most that compiles
 // without spills (128 VGPRs for 4): 4, but 3 for the two-set Q5_K and Q6_K
 // kernels, for GGUF-layout Q5_K / Q6_K and for Q4_K / Q5_K / Q6_K with two
-// row sets per workgroup.
+// row sets per workgroup, and 2 for GGUF-layout Q6_K with two row sets (185
+// VGPRs with its shifted chunk loads; its 8-wave launches take 104 KB of LDS,
+// so one workgroup per CU runs 2 waves per SIMD in any case).
 template <class T, int PK, int LAYOUT, int RS>
 constexpr int mm_waves_per_eu() {
+    if (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2 && RS == 2) return 2;
     return (T::kWide || (RS == 2 && T::kAux)) && (PK == 2 || RS == 2 || LAYOUT == M27Q_LAYOUT_GGUF) ? 3 : 4;
 }
 // GGUF-layout weights (LAYOUT == M27Q_LAYOUT_GGUF; Q4_K, Q5_K and Q6_K): the
@@ -1174,21 +1178,21 @@ static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipEr
 // against 28.8 with one-set tiles.  One-set tiles (more than 8 tokens left)
 // take two row sets per workgroup (RS = 2), each wave's activation operands
 // serving both: at M = 16 q/k/v 9.6 us against 10.4, o 10.1 against 11.5,
-// down 27.4 against 28.2; gate/up at M = 12 30.1 against 32.0.  GGUF-layout
-// Q6_K keeps one set per workgroup (its shifted chunk loads do not fit the
-// registers of two).  One set per workgroup splits K over 8 waves also on
-// K <= 6144 (at M = 16 gate/up 35.6 us against 37.7).
+// down 27.4 against 28.2; gate/up at M = 12 30.1 against 32.0; GGUF-layout
+// down 32.6 against 35.5 at M = 16, 31.3 against 32.6 at M = 12.  One set per
+// workgroup split K over 8 waves also on K <= 6144 (at M = 16 gate/up 35.6 us
+// against 37.7).
 constexpr int kPk2MinSets = 128;
 template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
-    constexpr int RS = PK == 1 && !(LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) ? 2 : 1;
+    constexpr int RS = PK == 1 ? 2 : 1;
     constexpr int SR = 16 * PK * RS;
     long long wgs = 0;
     for (int i = 0; i < p.nmat; ++i) wgs += (p.rc[i] + SR - 1) / SR;
     if constexpr (PK == 2) {
         return launch_mfma_t<T, 2, 8, LAYOUT, RS>(p, m0, s);
     } else {
-        const int ks = (wgs < 320 || (RS == 1 && p.K <= 6144)) ? 8 : 4;
+        const int ks = wgs < 320 ? 8 : 4;
         return ks == 8 ? launch_mfma_t<T, 1, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, 1, 4, LAYOUT, RS>(p, m0, s);
     }
 }
