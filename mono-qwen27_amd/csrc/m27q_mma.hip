@@ -1183,13 +1183,15 @@ static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipEr
 // workgroup split K over 8 waves also on K <= 6144 (at M = 16 gate/up 35.6 us
 // against 37.7).
 constexpr int kPk2MinSets = 128;
-// Two-set Q6_K launches of at most one workgroup per CU (down: 160 of 32
-// rows) split K over 12 waves: their 8-wave workgroups (85 KB of staging
-// areas) run one per CU anyway, and 12 (128 KB, 3 waves per SIMD) shorten
-// each wave's unit chain from 8.5 to 5.7 units: down at M = 4 / 8 20.7 / 21.6
-// us against 22.5 / 23.1 (GGUF layout unchanged, 26.9 / 27.6 against 26.8 /
-// 27.8).  The same for Q4_K's q/k/v and o was slower (q/k/v 7.5 against 7.2
-// us).
+// Q6_K launches of at most one workgroup per CU (down: 160 of 32 rows) split
+// K over 12 waves: their 8-wave workgroups (85 KB of staging areas for
+// two-set tiles, 105 KB for two row sets of one-set tiles) run one per CU
+// anyway, and 12 (128 / 157 KB, 3 waves per SIMD) shorten each wave's unit
+// chain from 8.5 to 5.7 units: down at M = 4 / 8 20.7 / 21.6 us against
+// 22.5 / 23.1, at M = 12 / 16 25.5 / 26.8 against 26.9 / 28.2 (GGUF layout
+// at M <= 8 unchanged, 26.9 / 27.6 against 26.8 / 27.8; its one-set kernel
+// spills at 12 waves and keeps 8).  The same for Q4_K's q/k/v and o was
+// slower at M <= 8 (q/k/v 7.5 against 7.2 us) and equal at M = 16.
 constexpr long long kQ6Wide12MaxWgs = 256;
 template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
@@ -1202,6 +1204,8 @@ static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t
             if (wgs <= kQ6Wide12MaxWgs) return launch_mfma_t<T, 2, 12, LAYOUT, RS>(p, m0, s);
         return launch_mfma_t<T, 2, 8, LAYOUT, RS>(p, m0, s);
     } else {
+        if constexpr (std::is_same<T, MmQ6K>::value && LAYOUT == M27Q_LAYOUT_TILED)
+            if (wgs <= kQ6Wide12MaxWgs) return launch_mfma_t<T, 1, 12, LAYOUT, RS>(p, m0, s);
         const int ks = wgs < 320 ? 8 : 4;
         return ks == 8 ? launch_mfma_t<T, 1, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, 1, 4, LAYOUT, RS>(p, m0, s);
     }
@@ -1228,7 +1232,8 @@ static hipError_t launch_mfma_cfg(const MatmulMultiParams &p, hipStream_t s) {
 template <class T>
 static size_t mfma_lds_max() {
     return std::max({mfma_lds<T, 1, 8>(), mfma_lds<T, 2, 8>(), mfma_lds<T, 1, 8, 2>(),
-                     std::is_same<T, MmQ6K>::value ? mfma_lds<T, 2, 12>() : (size_t)0});
+                     std::is_same<T, MmQ6K>::value ? mfma_lds<T, 2, 12>() : (size_t)0,
+                     std::is_same<T, MmQ6K>::value ? mfma_lds<T, 1, 12, 2>() : (size_t)0});
 }
 
 size_t matmul_mfma_lds_bytes(uint32_t type) {
