@@ -105,7 +105,8 @@ M27Q_API m27q_status m27q_unpack(uint32_t ggml_type, uint32_t row_blocks, uint32
 /* Re-tile a .m27b weight blob (include/mono27b_format.h:30-84) at pack time:
  * out_path gets a copy of in_path in which every matrix entry of a type with
  * a TILED form (whole GGUF rows) is re-tiled, its data_bytes updated and its
- * reserved field set to M27Q_LAYOUT_TILED; tensors are 256-byte aligned in the
+ * reserved field set to M27Q_LAYOUT_TILED | 2 << 16 (the high 16 bits: the
+ * revision of the TILED byte order); tensors are 256-byte aligned in the
  * file; the header, tokenizer section and all other tensors are copied.  The
  * result passes the reference's mono27b_validate_blob_file and
  * mono27b_read_weights_section.  Entries already tagged TILED are copied.
@@ -116,8 +117,9 @@ M27Q_API m27q_status m27q_retile_blob(const char *in_path, const char *out_path)
 /* One tensor of a .m27b weights section as a loader needs it: the entry's
  * fields (include/mono27b_format.h:74-84), the layout from its reserved field,
  * row_blocks as WeightView counts it (K / block size; K for F16 / F32; 0 when
- * the entry's byte count is not whole rows of its type in its layout), and the
- * absolute file offset of its bytes. */
+ * the entry's byte count is not whole rows of its type in its layout, or when
+ * a TILED entry carries another revision of the byte order), and the absolute
+ * file offset of its bytes. */
 typedef struct m27q_blob_tensor {
     char name[64];
     uint32_t ggml_type;
@@ -125,7 +127,7 @@ typedef struct m27q_blob_tensor {
     uint32_t role;
     uint32_t row_elems;
     uint32_t row_count;
-    uint32_t layout;       /* M27Q_LAYOUT_GGUF or M27Q_LAYOUT_TILED (entry.reserved) */
+    uint32_t layout;       /* M27Q_LAYOUT_GGUF or M27Q_LAYOUT_TILED (entry.reserved & 0xffff) */
     uint32_t row_blocks;
     uint32_t pad;
     uint64_t file_offset;

@@ -7,7 +7,8 @@
 // the weights section).  Its loader uploads those bytes verbatim (lw(),
 // exec:1695-1716).  m27q_retile_blob writes a copy whose quantized matrix
 // entries hold the TILED layout instead, with the layout tag in the entry's
-// reserved field (0 GGUF, 1 TILED) and each tensor 256-byte aligned; every
+// reserved field (0 GGUF; TILED: 1 in the low 16 bits, the revision of the
+// TILED byte order in the high 16) and each tensor 256-byte aligned; every
 // other byte (header fields, tokenizer, non-matrix tensors) is copied.  The
 // result still passes the reference's own blob validation and entry reads.
 // m27q_blob_tensors / m27q_blob_load are the loader's side: the entry table
@@ -90,6 +91,11 @@ bool zeros(const File &out, uint64_t n) {
     return true;
 }
 
+// Revision 2: the Q4_K / Q5_K qs plane chunk pair first.  A TILED entry of
+// another revision is listed with row_blocks 0, which m27q_blob_load refuses.
+constexpr uint32_t kTiledRevision = 2;
+constexpr uint32_t kTiledTag = M27Q_LAYOUT_TILED | kTiledRevision << 16;
+
 constexpr uint32_t kMaxRows = 1u << 24;   // the products' row limit
 constexpr uint32_t kMaxRowElems = 1u << 20;
 
@@ -154,7 +160,7 @@ m27q_status retile(const char *in_path, const char *out_path) {
     for (WeightEntry &e : outs) {
         pos = (pos + kAlign - 1) / kAlign * kAlign;
         if (retilable(e)) {
-            e.reserved = M27Q_LAYOUT_TILED;
+            e.reserved = kTiledTag;
             e.data_bytes = tiled_bytes(e.ggml_type, e.row_elems / block_elems(e.ggml_type), e.row_count);
         }
         e.data_offset = pos;
@@ -180,7 +186,7 @@ m27q_status retile(const char *in_path, const char *out_path) {
     for (size_t i = 0; i < ents.size(); ++i) {
         const WeightEntry &e = ents[i], &o = outs[i];
         if (!zeros(out, o.data_offset - at)) return M27Q_ERR_IO;
-        if (o.reserved == M27Q_LAYOUT_TILED && e.reserved != M27Q_LAYOUT_TILED) {
+        if (o.reserved == kTiledTag && e.reserved == M27Q_LAYOUT_GGUF) {
             src.resize((size_t)e.data_bytes);
             dst.resize((size_t)o.data_bytes);
             const uint32_t rb = e.row_elems / block_elems(e.ggml_type);
@@ -205,7 +211,7 @@ uint32_t entry_row_blocks(const WeightEntry &e) {
     if (be == 0 || e.row_elems % (uint32_t)be) return 0;
     const uint32_t rb = e.row_elems / (uint32_t)be;
     uint64_t want = 0;
-    if (e.reserved == M27Q_LAYOUT_TILED) {
+    if (e.reserved == kTiledTag) {
         if (!is_quant(e.ggml_type)) return 0;
         want = tiled_bytes(e.ggml_type, rb, e.row_count);
     } else if (e.reserved == M27Q_LAYOUT_GGUF) {
@@ -231,7 +237,7 @@ m27q_status tensors(const char *path, m27q_blob_tensor *out, int cap, int *count
         o.role = e.role;
         o.row_elems = e.row_elems;
         o.row_count = e.row_count;
-        o.layout = e.reserved;
+        o.layout = e.reserved & 0xffffu;
         o.row_blocks = entry_row_blocks(e);
         o.file_offset = t.secs[t.wi].offset + e.data_offset;
         o.bytes = e.data_bytes;

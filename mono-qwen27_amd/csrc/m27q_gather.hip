@@ -42,13 +42,13 @@ __device__ __forceinline__ Raw load_q4k(const GatherParams &p, int r, int b, int
         const uint8_t *unit = p.W + ((size_t)(r / kTileRows) * p.upr + b) * kQ4KUnit;
         const int i = r % kTileRows;
         hdr = unit + 16 * i;
-        qs = unit + 128 + 128 * i;
+        qs = unit + q4k_tqs(i, g);  // qs bytes [32 g, 32 g + 32)
     } else {
         hdr = p.W + ((size_t)r * p.rb + b) * kQ4KBytes;
-        qs = hdr + kQ4KHdr;
+        qs = hdr + kQ4KHdr + 32 * g;
     }
     w.a = *(const uint4 *)hdr;
-    w.b = *(const uint32_t *)(qs + 32 * g + lq);
+    w.b = *(const uint32_t *)(qs + lq);
     return w;
 }
 __device__ __forceinline__ float4 cvt_q4k(const Raw &w, int l) {
@@ -72,15 +72,15 @@ __device__ __forceinline__ Raw load_q5k(const GatherParams &p, int r, int b, int
         const uint8_t *unit = p.W + ((size_t)(r / kTileRows) * p.upr + b) * kQ5KUnit;
         const int i = r % kTileRows;
         hdr = unit + 16 * i;
-        qs = unit + 128 + 128 * i;
+        qs = unit + q4k_tqs(i, g);  // qs bytes [32 g, 32 g + 32)
         qh = unit + kQ5KTQh + 32 * i;
     } else {
         hdr = p.W + ((size_t)r * p.rb + b) * kQ5KBytes;
-        qs = hdr + kQ5KQs;
+        qs = hdr + kQ5KQs + 32 * g;
         qh = hdr + kQ5KQh;
     }
     w.a = *(const uint4 *)hdr;
-    w.b = *(const uint32_t *)(qs + 32 * g + lq);
+    w.b = *(const uint32_t *)(qs + lq);
     w.c = *(const uint32_t *)(qh + lq);
     return w;
 }

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int NR = TPW * kTileRows;  // rows per workgroup
-    const int lane = (int)(threadIdx.x & 63), i = lane >> 3, c = lane & 7;
+    using LM = LaneMap<T, LAYOUT>;
+    const int lane = (int)(threadIdx.x & 63), i = LM::row(lane), c = LM::chunk(lane);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int ks = wave % KS, tg = wave / KS;  // K slice and tile group of this wave
     const int nth = C::NW * kWave;
@@ -292,7 +293,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_q8(GemvParams p) {
     for (int mm = 0; mm < NM; ++mm)
 #pragma unroll
         for (int t = 0; t < WT; ++t) {
-            const float r = sum8(acc[mm][t]);
+            const float r = LM::sum(acc[mm][t]);
             if (c == 0) red[(mm * KS + ks) * NR + (tg * WT + t) * kTileRows + i] = r;
         }
     __syncthreads();
@@ -332,7 +333,7 @@ struct TileSrc {
     int rb, i, c;
     typename T::Lane L;
     __device__ TileSrc(const uint8_t *W, int tile, int row, int rb_, int upr, int lane)
-        : rb(rb_), i(lane >> 3), c(lane & 7), L(lane & 7) {
+        : rb(rb_), i(LaneMap<T, LAYOUT>::row(lane)), c(LaneMap<T, LAYOUT>::chunk(lane)), L(LaneMap<T, LAYOUT>::chunk(lane)) {
         if (LAYOUT == M27Q_LAYOUT_TILED) base = W + (size_t)tile * upr * T::kUnitBytes;
         else base = W + (size_t)row * rb_ * T::kBlockBytes;
     }
@@ -386,7 +387,8 @@ __global__ __launch_bounds__(256) void k_gemv_f32(GemvParams p) {
     __syncthreads();
     const ActLdsF32 act{xf, x16};
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane >> 3, c = lane & 7;
+    using LM = LaneMap<T, LAYOUT>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = LM::row(lane), c = LM::chunk(lane);
     const int rc = p.rc[0];
     const int tile = (int)blockIdx.x * kWavesPerWG + wave;
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(GemvParams p) {
         const TileSrc<T, LAYOUT> src(p.W[0], tile, row_ld, p.rb, p.upr, lane);
         acc = stream_row_f32<T, LAYOUT, 2>(src, act, p.upr);
     }
-    acc = sum8(acc);
+    acc = LM::sum(acc);
     if (c == 0 && tile < ntiles && row < rc) p.y[0][row] = acc + (p.res[0] ? p.res[0][row] : 0.f);
 }
 

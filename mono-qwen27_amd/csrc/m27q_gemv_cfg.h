@@ -84,8 +84,9 @@ using CfgQ = GemvCfg<2, 4, 2, 1>;
 using Cfg161 = GemvCfg<16, 1, 1, 1>;
 using Cfg822 = GemvCfg<8, 2, 2, 0>;
 using CfgB = GemvCfg<4, 3, 1, 1>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
-using CfgB9 = GemvCfg<4, 9, 3, 1>;  // balanced tiling for 8-9 tiles per CU (config 1); swept against
-                                     // (5, 9, 3) equal, (3, 9, 3) +0.6, (2, 9, 3) +1.1, (1, 9, 1) +1.6 us
+using CfgB9 = GemvCfg<5, 9, 3, 1>;  // balanced tiling for 8-9 tiles per CU (config 1); swept against
+                                     // (4, 9, 3) +0.3, (3, 9, 3) +0.5, (8, 9, 9) +0.4, (4, 9, 9) +1.8,
+                                     // (2, 9, 3) +1.5 us
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
 static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 

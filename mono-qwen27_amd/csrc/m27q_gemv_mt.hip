@@ -24,7 +24,8 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KS = C::KS, TPW = C::TPW, WT = C::WT;
     constexpr int NR = TPW * kTileRows;  // rows per workgroup
-    const int lane = (int)(threadIdx.x & 63), i = lane >> 3, c = lane & 7;
+    using LM = LaneMap<T, LAYOUT>;
+    const int lane = (int)(threadIdx.x & 63), i = LM::row(lane), c = LM::chunk(lane);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int ks = wave % KS, tg = wave / KS;
     const int nth = C::NW * kWave;
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(kWave *C::NW) void k_gemv_mt(MatmulMultiParams p, i
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int t = 0; t < WT; ++t) {
-            const float r = sum8(acc[mt][t]);
+            const float r = LM::sum(acc[mt][t]);
             if (c == 0) red[(mt * KS + ks) * NR + (tg * WT + t) * kTileRows + i] = r;
         }
     __syncthreads();

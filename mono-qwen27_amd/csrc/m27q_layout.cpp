@@ -13,28 +13,31 @@ using namespace m27q;
 namespace {
 
 // Copy one GGUF block <-> its slots in a tiled unit.  dir = true: GGUF -> tiled.
-void move_q4k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
-    uint8_t *hdr = unit + 16 * i, *qs = unit + 128 + 128 * i;
-    if (to_tiled) {
-        std::memcpy(hdr, blk, kQ4KHdr);
-        std::memcpy(qs, blk + kQ4KHdr, 128);
-    } else {
-        std::memcpy(blk, hdr, kQ4KHdr);
-        std::memcpy(blk + kQ4KHdr, qs, 128);
+// The 128 qs bytes of row i <-> their four 32-byte chunk pairs in the unit.
+void move_qs_pairs(uint8_t *unit, int i, uint8_t *qs, bool to_tiled) {
+    for (int g = 0; g < 4; ++g) {
+        if (to_tiled) std::memcpy(unit + q4k_tqs(i, g), qs + 32 * g, 32);
+        else std::memcpy(qs + 32 * g, unit + q4k_tqs(i, g), 32);
     }
 }
 
+void move_q4k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
+    uint8_t *hdr = unit + 16 * i;
+    if (to_tiled) std::memcpy(hdr, blk, kQ4KHdr);
+    else std::memcpy(blk, hdr, kQ4KHdr);
+    move_qs_pairs(unit, i, blk + kQ4KHdr, to_tiled);
+}
+
 void move_q5k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {
-    uint8_t *hdr = unit + 16 * i, *qs = unit + 128 + 128 * i, *qh = unit + kQ5KTQh + 32 * i;
+    uint8_t *hdr = unit + 16 * i, *qh = unit + kQ5KTQh + 32 * i;
     if (to_tiled) {
         std::memcpy(hdr, blk, kQ4KHdr);
         std::memcpy(qh, blk + kQ5KQh, 32);
-        std::memcpy(qs, blk + kQ5KQs, 128);
     } else {
         std::memcpy(blk, hdr, kQ4KHdr);
         std::memcpy(blk + kQ5KQh, qh, 32);
-        std::memcpy(blk + kQ5KQs, qs, 128);
     }
+    move_qs_pairs(unit, i, blk + kQ5KQs, to_tiled);
 }
 
 void move_q6k(uint8_t *unit, int i, uint8_t *blk, bool to_tiled) {

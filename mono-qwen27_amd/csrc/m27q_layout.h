@@ -35,10 +35,11 @@ constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 //
 //  Q4_K  unit = one block column                          1152 B
 //        [0, 128)      8 x 16 B headers (d, dmin, scales[12])  row i at 16 i
-//        [128, 1152)   8 x 128 B qs                            row i at 128 + 128 i
+//        [128, 1152)   qs by 32-byte chunk pair g = 0..3, then row:
+//                      qs[32 g, 32 g + 32) of row i at 128 + 256 g + 32 i
 //  Q5_K  unit = one block column                          1408 B
 //        [0, 128)      8 x 16 B headers (d, dmin, scales[12])  row i at 16 i
-//        [128, 1152)   8 x 128 B qs                            row i at 128 + 128 i
+//        [128, 1152)   qs as for Q4_K
 //        [1152, 1408)  8 x 32 B qh                             row i at 1152 + 32 i
 //  Q6_K  unit = one block column                          1680 B
 //        [0, 1024)     8 x 128 B ql                            row i at 128 i
@@ -55,6 +56,15 @@ constexpr int kQ6KQl = 0, kQ6KQh = 128, kQ6KSc = 192, kQ6KD = 208;
 // Unit (t, u) starts at (t * units_per_row + u) * unit_bytes.  Rows past
 // row_count in the last tile, and Q8_0 block columns past row_blocks in the
 // last unit, are zero blocks (d = 0, so they contribute exactly 0).
+//
+// The Q4_K / Q5_K qs plane is ordered chunk pair first so that both of its
+// readers get whole 128-byte lines per load: the M = 1 kernels read the 1 KiB
+// plane with one 16-byte load per lane (lane l takes bytes 16 l, i.e. row
+// (l / 2) % 8 and chunk 2 (l / 16) + l % 2), and the small-M MFMA kernels load
+// their operands straight into registers, where a lane needs the same 16 bytes
+// of 16 different rows: with one 128-byte row after another those loads touch
+// a line per row and run at half the streaming rate (measured on gfx950 over
+// 100 MB: 2.5-2.8 TB/s against 5.0-6.1 chunk pair first).
 constexpr int kTileRows = 8;
 constexpr int kLanesPerRow = 8;                    // GEMV: 8 lanes x 16 B per row and unit
 constexpr int kWavesPerWG = 4;                     // GEMV workgroup = 4 waves ...
@@ -62,6 +72,9 @@ constexpr int kRowsPerWG = kWavesPerWG * kTileRows;  // ... = 32 output rows
 constexpr int kQ4KUnit = kTileRows * kQ4KBytes;      // 1152
 constexpr int kQ5KUnit = kTileRows * kQ5KBytes;      // 1408
 constexpr int kQ5KTQh = 1152;
+constexpr int kQ4KTQs = 128;
+// Offset in a Q4_K / Q5_K unit of qs bytes [32 g, 32 g + 32) of row i.
+constexpr int q4k_tqs(int i, int g) { return kQ4KTQs + 256 * g + 32 * i; }
 constexpr int kQ6KUnit = kTileRows * kQ6KBytes;      // 1680
 constexpr int kIQ4XSUnit = kTileRows * kIQ4XSBytes;  // 1088
 constexpr int kIQ4XSTHdr = 1024;

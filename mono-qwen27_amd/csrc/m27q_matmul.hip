@@ -21,7 +21,8 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
     float *xd = (float *)(smem + MT * CK);           // [MT][CK/32]
     uint32_t *xs = (uint32_t *)(xd + MT * CK / 32);  // [MT][CK/32 * T::kAuxWords]
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane >> 3, c = lane & 7;
+    using LM = LaneMap<T, LAYOUT>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = LM::row(lane), c = LM::chunk(lane);
     const int rc = p.rc;
     const int tile = (int)blockIdx.x * kWavesPerWG + wave;
     const int ntiles = (rc + kTileRows - 1) / kTileRows;
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(256) void k_matmul_q8(MatmulParams p, int m0) {
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const float v = sum8(acc[m]);
+        const float v = LM::sum(acc[m]);
         if (c == 0 && tile < ntiles && row < rc && m0 + m < p.M) {
             const size_t o = (size_t)(m0 + m) * rc + row;
             p.Y[o] = v + (p.res ? p.res[o] : 0.f);

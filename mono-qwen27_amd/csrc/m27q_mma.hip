@@ -59,6 +59,7 @@ namespace m27q {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // staging registers (promoted; HIP's uint4 arrays are not)
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 template <int PK>
 struct Pack {
@@ -83,6 +84,10 @@ __device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; 
 template <int AUX = 0>
 __device__ __forceinline__ v4u buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+}
+template <int AUX = 0>
+__device__ __forceinline__ v2u buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, AUX));
 }
 // Measured on the layer's products at M = 4 / 8 / 16 (cold weights): 61.2 /
 // 63.4 / 82.3 us per layer with non-temporal weight loads against 64.0 / 66.6
@@ -153,6 +158,7 @@ struct MmQ4KT {
     // more live registers than 4 waves per SIMD allow at PK = 2 and in GGUF layout
     static constexpr bool kWide = Q5;
     static constexpr bool kPaired = true;
+    static constexpr bool kDirect = true;  // TILED operands straight from memory
     template <int PK>
     static constexpr int kPieces = PK;
     // The min term's token factor: dx * (sum of the 32 codes).
@@ -164,11 +170,15 @@ struct MmQ4KT {
         uint2 qh[Q5 ? PK : 1];
     };
     // LDS row record: header 16 | qs 128 (| Q5_K qh 32).  Chunk c (16 bytes)
-    // of the TILED unit of 8-row tile t goes to:
+    // of the TILED unit of 8-row tile t goes to (qs chunk q = c - 8 of the
+    // chunk-pair-first plane: row (q / 2) % 8, qs bytes 32 (q / 16) + 16 (q % 2)):
     static constexpr int kRowBytes = Q5 ? 176 : 144;
     __device__ static int lds_dst(int t, int c, int) {
         if (c < 8) return (8 * t + c) * kRowBytes;
-        if (c < 72) return (8 * t + ((c - 8) >> 3)) * kRowBytes + 16 + 16 * ((c - 8) & 7);
+        if (c < 72) {
+            const int q = c - 8;
+            return (8 * t + ((q >> 1) & 7)) * kRowBytes + 16 + 32 * (q >> 4) + 16 * (q & 1);
+        }
         return (8 * t + ((c - 72) >> 1)) * kRowBytes + 144 + 16 * ((c - 72) & 1);  // Q5_K qh
     }
     // GGUF layout: a row's block of the unit is kGgufChunks 16-byte chunks
@@ -204,6 +214,48 @@ struct MmQ4KT {
             } else {
                 f.qh[0] = ld8(rb + 144 + 8 * r);
             }
+        }
+    }
+    // TILED operands loaded straight into registers (kDirect): for the lane's
+    // row i of its tile and piece lane r, the 8 PK qs bytes 8 PK r .. of each
+    // chunk pair j (its pieces of groups 2 j and 2 j + 1), the row's header
+    // and (Q5_K) qh bytes 8 PK r ..; the chunk-pair-first qs plane puts the
+    // same bytes of a tile's 8 rows in one 256-byte run, so a wave's load
+    // reads whole 128-byte lines.
+    template <int PK>
+    using DVec = typename std::conditional<PK == 2, v4u, v2u>::type;
+    template <int PK>
+    struct Direct {
+        DVec<PK> q[4];
+        v4u h;
+        DVec<PK> qh[1];  // Q5_K only
+    };
+    template <int PK>
+    __device__ static DVec<PK> dld(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+        if constexpr (PK == 2) return buf_ld16<kWeightAux>(rs, voff, soff);
+        else return buf_ld8<kWeightAux>(rs, voff, soff);
+    }
+    template <int PK>
+    __device__ static void load_direct(Direct<PK> &d, __amdgpu_buffer_rsrc_t rs, uint32_t tile_off, int i, int r,
+                                       uint32_t soff) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d.q[j] = dld<PK>(rs, tile_off + (uint32_t)(q4k_tqs(i, j) + 8 * PK * r), soff);
+        d.h = buf_ld16<kWeightAux>(rs, tile_off + 16u * (uint32_t)i, soff);
+        if constexpr (Q5) d.qh[0] = dld<PK>(rs, tile_off + (uint32_t)(kQ5KTQh + 32 * i + 8 * PK * r), soff);
+    }
+    // The half unit's fragment from those registers, as load() reads it from LDS.
+    template <int PK>
+    __device__ static void frag_direct(Frag<PK> &f, const Direct<PK> &d, int st) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const DVec<PK> &v = d.q[2 * st + cc];
+            f.qs[cc][0] = make_uint2(v[0], v[1]);
+            if constexpr (PK == 2) f.qs[cc][1] = make_uint2(v[2], v[3]);
+        }
+        f.h = make_uint4(d.h.x, d.h.y, d.h.z, d.h.w);
+        if constexpr (Q5) {
+            f.qh[0] = make_uint2(d.qh[0][0], d.qh[0][1]);
+            if constexpr (PK == 2) f.qh[1] = make_uint2(d.qh[0][2], d.qh[0][3]);
         }
     }
     template <int PK, int ST>
@@ -272,6 +324,9 @@ struct MmQ6K {
     static constexpr int kPieces = 2;
     static constexpr bool kWide = true;
     static constexpr bool kPaired = false;  // MFMA m is sub-block m (its own scale)
+    static constexpr bool kDirect = false;
+    template <int PK>
+    struct Direct {};
     __device__ static float stage_aux(float, uint32_t) { return 0.f; }
     template <int PK>
     struct Frag {
@@ -373,6 +428,9 @@ struct MmQ80 {
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
     static constexpr bool kPaired = true;
+    static constexpr bool kDirect = false;
+    template <int PK>
+    struct Direct {};
     // TILED only (34-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
     static constexpr int kBlockBytes = kQ80Bytes, kGgufChunks = 0;
     static constexpr bool kGgufA2 = false;
@@ -438,6 +496,9 @@ struct MmIQ4XS {
     static constexpr bool kAux = false;
     static constexpr bool kWide = false;
     static constexpr bool kPaired = false;  // a piece is one nibble of 8 bytes
+    static constexpr bool kDirect = false;
+    template <int PK>
+    struct Direct {};
     // TILED only (136-byte GGUF blocks take the VALU kernel: matmul_mfma_takes)
     static constexpr int kBlockBytes = kIQ4XSBytes, kGgufChunks = 0;
     static constexpr bool kGgufA2 = false;
@@ -532,7 +593,8 @@ __device__ __forceinline__ void compute_half(const typename T::template Frag<PK>
 
 // Per-wave LDS staging area for one unit (bytes):
 //   W: 16 PK RS row records of T::kRowBytes (RS row sets per workgroup), then
-//      a side area (64 bytes per tile)
+//      a side area (64 bytes per tile); none where the weight operands are
+//      loaded straight into registers (DW)
 //   A: TK token records of 32 G + 16 bytes (G groups of codes + pad), then,
 //      for PK = 2 (and Q6_K's zero-split views), one record of zeros for the
 //      operand lanes of the other set (or sub-block)
@@ -541,11 +603,11 @@ __device__ __forceinline__ void compute_half(const typename T::template Frag<PK>
 // The paddings keep the MFMA-layout reads free of bank conflicts: the row
 // strides 144, 176, 240 and the token strides 272, 144 put the 16 rows (or
 // tokens) of a half wave on distinct 4-bank groups.
-template <class T, int PK, int RS = 1>
+template <class T, int PK, int RS = 1, bool DW = false>
 struct Stage {
     static constexpr int G = T::kGroups, TK = Pack<PK>::TK, UE = 32 * G, UB = T::kUnitBytes;
-    static constexpr int kSide = 16 * PK * RS * T::kRowBytes;
-    static constexpr int kW = kSide + 2 * PK * RS * 64;
+    static constexpr int kSide = DW ? 0 : 16 * PK * RS * T::kRowBytes;
+    static constexpr int kW = DW ? 0 : kSide + 2 * PK * RS * 64;
     static constexpr int kARow = UE + 16;
     static constexpr int oA = kW;
     static constexpr int oZero = oA + TK * kARow;
@@ -553,14 +615,16 @@ struct Stage {
     static constexpr int oS = oZero + (kZeroRec ? UE : 0);
     static constexpr int oDummy = oS + G * TK * 4 * (T::kAux ? 2 : 1);
     static constexpr int kBytes = (oDummy + 16 + 15) / 16 * 16;
-    static constexpr int kWChunks = 2 * PK * RS * UB / 16;  // 16-byte chunks of the sets' unit
+    static constexpr int kWChunks = DW ? 0 : 2 * PK * RS * UB / 16;  // 16-byte chunks of the sets' unit
     static constexpr int kNW = (kWChunks + kWave - 1) / kWave;
+    static constexpr int kNWR = kNW > 0 ? kNW : 1;  // staging register arrays
     static constexpr int kAChunks = TK * UE / 16;
     static constexpr int kNA = (kAChunks + kWave - 1) / kWave;
     static constexpr int kSLanes = TK * G / 4;  // lanes staging 4 scales each
     static_assert(kSLanes <= kWave, "scale staging lanes");
     static_assert(kAChunks % kWave == 0, "whole activation staging rounds");
     static_assert(UB % 16 == 0 && kARow % 16 == 0 && T::kRowBytes % 16 == 0, "16-byte staging");
+    static_assert(kBytes >= RS * 4 * kWave * 4, "the partial sums fit the wave areas");
 };
 
 // One workgroup: RS row sets of 16 PK rows of one matrix (RS = 2 only with
@@ -579,6 +643,7 @@ struct Stage {
 template <class T, int PK, int LAYOUT, int RS>
 constexpr int mm_waves_per_eu() {
     if (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2 && RS == 2) return 2;
+    if (LAYOUT == M27Q_LAYOUT_TILED && T::kDirect) return T::kWide && RS == 2 ? 2 : 3;
     return (T::kWide || (RS == 2 && T::kAux)) && (PK == 2 || RS == 2 || LAYOUT == M27Q_LAYOUT_GGUF) ? 3 : 4;
 }
 // GGUF-layout weights (LAYOUT == M27Q_LAYOUT_GGUF; Q4_K, Q5_K and Q6_K): the
@@ -601,8 +666,9 @@ template <class T, int PK, int KS, int LAYOUT, int RS>
 __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) void k_matmul_mfma(
     MatmulMultiParams p, int m0) {
     extern __shared__ __align__(16) uint8_t smem[];
-    using SG = Stage<T, PK, RS>;
     constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;
+    constexpr bool kD = !kG && T::kDirect;  // TILED weight operands straight into registers
+    using SG = Stage<T, PK, RS, kD>;
     constexpr int SR = 16 * PK * RS;  // rows of the workgroup
     static_assert(RS == 1 || PK == 1, "two row sets per workgroup only with one-set tiles");
     static_assert(!kG || SR * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
@@ -634,8 +700,8 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     // scalar register (a TILED matrix is below 4 GiB: the host checks it).
     // Reads past the activation codes (the last Q8_0 unit past K) return
     // zeros; their groups have zero scales.
-    uint32_t goff[SG::kNW];
-    int wdst[SG::kNW];
+    uint32_t goff[SG::kNWR];
+    int wdst[SG::kNWR];
     constexpr int UBW = kG ? T::kBlockBytes : UB;  // weight bytes of one unit per tile (GGUF: per row)
     const uint32_t rowb = (uint32_t)p.upr * (uint32_t)T::kBlockBytes;  // GGUF row bytes
 #pragma unroll
@@ -682,7 +748,7 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     const uint32_t sbytes = (uint32_t)p.M * (uint32_t)ngroups * 4u;
     const __amdgpu_buffer_rsrc_t dr = buf_rsrc(p.xd, sbytes), sr = buf_rsrc(p.xs, sbytes);
     constexpr bool kA2 = kG && T::kGgufA2;
-    v4u rw[SG::kNW], ra[SG::kNA];
+    v4u rw[SG::kNWR], ra[SG::kNA];
     uint32_t re[kA2 ? SG::kNW : 1], rsh[kA2 ? SG::kNW : 1], rd = 0u;
     float sd[4];
     uint32_t ss[4] = {0u, 0u, 0u, 0u};
@@ -765,6 +831,25 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     }
     const ScaleLds<PK> sl{(const float *)(wl + SG::oS), (const float *)(wl + SG::oS) + G * TK};
 
+    // Direct operands: row set r's row of this lane (rows past the matrix
+    // reread the last tile; their outputs are dropped), as the tile's offset
+    // and the row within it.
+    uint32_t dtile[RS];
+    int drow[RS];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        const int R = row0 + wrow + 16 * r;
+        dtile[r] = (uint32_t)min(R / kTileRows, ntiles8 - 1) * (uint32_t)(p.upr * UB);
+        drow[r] = R % kTileRows;
+    }
+    typename T::template Direct<PK> dc[RS], dn[RS];
+    auto dload = [&](int u, typename T::template Direct<PK>(&d)[RS]) __attribute__((always_inline)) {
+        if constexpr (kD) {
+#pragma unroll
+            for (int r = 0; r < RS; ++r) T::template load_direct<PK>(d[r], wr, dtile[r], drow[r], L.r, (uint32_t)u * UB);
+        }
+    };
+
     float acc[RS][4], u4[RS][4];
     v4f cm[RS];  // Q4_K min term
 #pragma unroll
@@ -787,7 +872,10 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
 #pragma unroll
         for (int r = 0; r < RS; ++r) {
             typename T::template Frag<PK> f;
-            T::template load<PK>(f, wl, wrow + 16 * r, L.r, ST, SG::kSide);
+            if constexpr (kD)
+                T::template frag_direct<PK>(f, dc[r], ST);
+            else
+                T::template load<PK>(f, wl, wrow + 16 * r, L.r, ST, SG::kSide);
             compute_half<T, PK, ST>(f, x, sl, 0, L, areal, atok, acc[r], u4[r], cm[r]);
             if (r + 1 < RS) __builtin_amdgcn_sched_barrier(0);
         }
@@ -803,13 +891,21 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
     // compiler wait for every load before each use); the last unit is peeled.
     // A wave's LDS reads and writes are executed in order, so a unit's
     // staging writes follow the previous unit's operand reads.
+    // Direct operands: the next unit's weights are loaded after its
+    // activations, so the staging writes wait only for the activations.
     if (nu > 0) {
         issue(ub);
+        dload(ub, dc);
         commit(ub);
         for (int k = 0; k + 1 < nu; ++k) {
             issue(ub + k + 1);
+            dload(ub + k + 1, dn);
             compute();
             commit(ub + k + 1);
+            if constexpr (kD) {
+#pragma unroll
+                for (int r = 0; r < RS; ++r) dc[r] = dn[r];
+            }
         }
         compute();
     }
@@ -1108,14 +1204,14 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
     }
 }
 
-template <class T, int PK, int KS, int RS = 1>
+template <class T, int PK, int KS, int RS = 1, bool DW = false>
 static size_t mfma_lds() {
-    return (size_t)KS * Stage<T, PK, RS>::kBytes;
+    return (size_t)KS * Stage<T, PK, RS, DW>::kBytes;
 }
 
 template <class T, int PK, int KS, int LAYOUT, int RS>
 static hipError_t launch_mfma_t(MatmulMultiParams p, int m0, hipStream_t s) {
-    const size_t lds = mfma_lds<T, PK, KS, RS>();
+    const size_t lds = mfma_lds<T, PK, KS, RS, LAYOUT == M27Q_LAYOUT_TILED && T::kDirect>();
     constexpr int SR = 16 * PK * RS;
     int total = 0;
     for (int i = 0; i < p.nmat; ++i) {
@@ -1160,11 +1256,15 @@ static bool launch_xres_t(MatmulMultiParams p, int m0, hipStream_t s, hipError_t
     return true;
 }
 // GGUF-layout Q6_K's shifted chunk loads do not fit the resident kernel's 128
-// registers without spilling: those launches take the per-unit kernel.
+// registers without spilling: those launches take the per-unit kernel.  So do
+// TILED Q4_K / Q5_K, whose per-unit kernel loads the weight operands straight
+// into registers: gate/up at M = 16 31.4 us against 32.9 resident.
 template <class T, int LAYOUT>
 static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipError_t *err) {
-    if constexpr (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) return false;
-    else return launch_xres_t<T, LAYOUT>(p, m0, s, err);
+    if constexpr ((LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) || (LAYOUT == M27Q_LAYOUT_TILED && T::kDirect))
+        return false;
+    else
+        return launch_xres_t<T, LAYOUT>(p, m0, s, err);
 }
 
 // Launch shape, from sweeps of the Qwen-27B layer at M = 4, 8, 12, 16:
@@ -1193,6 +1293,7 @@ constexpr int kPk2MinSets = 128;
 // spills at 12 waves and keeps 8).  The same for Q4_K's q/k/v and o was
 // slower at M <= 8 (q/k/v 7.5 against 7.2 us) and equal at M = 16.
 constexpr long long kQ6Wide12MaxWgs = 256;
+constexpr long long kDirectKs4MinWgs = 320;
 template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
     constexpr int RS = PK == 1 ? 2 : 1;
@@ -1202,6 +1303,8 @@ static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t
     if constexpr (PK == 2) {
         if constexpr (std::is_same<T, MmQ6K>::value)
             if (wgs <= kQ6Wide12MaxWgs) return launch_mfma_t<T, 2, 12, LAYOUT, RS>(p, m0, s);
+        if constexpr (LAYOUT == M27Q_LAYOUT_TILED && T::kDirect)
+            if (wgs >= kDirectKs4MinWgs) return launch_mfma_t<T, 2, 4, LAYOUT, RS>(p, m0, s);
         return launch_mfma_t<T, 2, 8, LAYOUT, RS>(p, m0, s);
     } else {
         if constexpr (std::is_same<T, MmQ6K>::value && LAYOUT == M27Q_LAYOUT_TILED)

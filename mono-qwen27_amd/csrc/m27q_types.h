@@ -1,11 +1,13 @@
 // m27q_types.h -- per-type lane fragments for the gfx950 GEMV kernels.
 //
 // Work mapping shared by every GEMV kernel: a wavefront owns a tile of 8 rows;
-// lane = 8 * i + c works on row i and on the c-th 16-byte chunk of that row's
+// each lane works on one row i and on the c-th 16-byte chunk of that row's
 // quants in the current unit (one 256-weight block for Q4_K / Q6_K, four
-// 32-weight blocks for Q8_0).  One unit of 8 rows is therefore read by one
-// 16-byte-per-lane load per plane: 1 KiB of contiguous bytes per instruction
-// in the TILED layout.
+// 32-weight blocks for Q8_0): lane = 8 i + c, or, for the chunk-pair-first
+// Q4_K / Q5_K qs plane of the TILED layout, lane = 16 (c / 2) + 2 i + c % 2
+// (LaneMap).  One unit of 8 rows is therefore read by one 16-byte-per-lane
+// load per plane: 1 KiB of contiguous bytes per instruction in the TILED
+// layout.
 //
 // Activations are staged in LDS by the calling kernel:
 //   int8  xc[Kp]       codes (Kp = K padded to whole units, pad = 0)
@@ -43,6 +45,7 @@ __device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float)((w 
 // the min term of pair j = c for the whole block.
 struct Q4K {
     static constexpr uint32_t kType = kQ4_K;
+    static constexpr bool kChunkMajor = true;  // TILED qs plane chunk pair first
     static constexpr int kUnitElems = 256;
     static constexpr int kUnitBytes = kQ4KUnit;
     static constexpr int kBlockBytes = kQ4KBytes;
@@ -85,9 +88,16 @@ struct Q4K {
         float dsum;
     };
 
+    __device__ static int qs_chunk(int i, int c) { return q4k_tqs(i, c >> 1) + 16 * (c & 1); }
     template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
-        return {ld_u128<NT>(unit + 128 + 128 * i + 16 * c), ld_u128<NT>(unit + 16 * i)};
+        return {ld_u128<NT>(unit + qs_chunk(i, c)), ld_u128<NT>(unit + 16 * i)};
+    }
+    // The same for the GEMV's lane order over the plane (LaneMap): lane l
+    // reads qs plane bytes 16 l, its row i's header.
+    template <bool NT = false>
+    __device__ static Frag load_tiled_lane(const uint8_t *unit, int lane, int i) {
+        return {ld_u128<NT>(unit + kQ4KTQs + 16 * lane), ld_u128<NT>(unit + 16 * i)};
     }
     template <bool NT = false>
     __device__ static Frag load_gguf(const uint8_t *row, int u, int /*rb*/, int c, const Lane &) {
@@ -97,7 +107,7 @@ struct Q4K {
     // The same planes through a buffer descriptor of the tile; soff = the unit's offset.
     template <int AUX>
     __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &) {
-        return {bld_u128<AUX>(r, 128 + 128 * i + 16 * c, soff), bld_u128<AUX>(r, 16 * i, soff)};
+        return {bld_u128<AUX>(r, qs_chunk(i, c), soff), bld_u128<AUX>(r, 16 * i, soff)};
     }
 
     // 6-bit scales of pairs 2g, 2g+1 (bits 0-5 and 8-13) and the min of pair c.
@@ -199,7 +209,13 @@ struct Q5K : Q4K {
 
     template <bool NT = false>
     __device__ static Frag load_tiled(const uint8_t *unit, int i, int c, const Lane &) {
-        return {ld_u128<NT>(unit + 128 + 128 * i + 16 * c), ld_u128<NT>(unit + kQ5KTQh + 32 * i + 16 * (c & 1)),
+        return {ld_u128<NT>(unit + qs_chunk(i, c)), ld_u128<NT>(unit + kQ5KTQh + 32 * i + 16 * (c & 1)),
+                ld_u128<NT>(unit + 16 * i)};
+    }
+    // GEMV lane order (LaneMap): qs plane bytes 16 l; qh bytes 16 (l % 2) of row i = (l / 2) % 8.
+    template <bool NT = false>
+    __device__ static Frag load_tiled_lane(const uint8_t *unit, int lane, int i) {
+        return {ld_u128<NT>(unit + kQ4KTQs + 16 * lane), ld_u128<NT>(unit + kQ5KTQh + 16 * (lane & 15)),
                 ld_u128<NT>(unit + 16 * i)};
     }
     template <bool NT = false>
@@ -209,7 +225,7 @@ struct Q5K : Q4K {
     }
     template <int AUX>
     __device__ static Frag load_tiled_buf(__amdgpu_buffer_rsrc_t r, uint32_t soff, int i, int c, const Lane &) {
-        return {bld_u128<AUX>(r, 128 + 128 * i + 16 * c, soff), bld_u128<AUX>(r, kQ5KTQh + 32 * i + 16 * (c & 1), soff),
+        return {bld_u128<AUX>(r, qs_chunk(i, c), soff), bld_u128<AUX>(r, kQ5KTQh + 32 * i + 16 * (c & 1), soff),
                 bld_u128<AUX>(r, 16 * i, soff)};
     }
 
@@ -267,6 +283,7 @@ struct Q5K : Q4K {
 // (exec:1026-1048 for the index map).
 struct Q6K {
     static constexpr uint32_t kType = kQ6_K;
+    static constexpr bool kChunkMajor = false;
     static constexpr int kUnitElems = 256;
     static constexpr int kUnitBytes = kQ6KUnit;
     static constexpr int kBlockBytes = kQ6KBytes;
@@ -424,6 +441,7 @@ struct Q6K {
 // (vec_dot_iq4_xs_q8_1, exec:647-671).  GGUF blocks are 136 B: 8-byte loads.
 struct IQ4XS {
     static constexpr uint32_t kType = kIQ4_XS;
+    static constexpr bool kChunkMajor = false;
     static constexpr int kUnitElems = 256;
     static constexpr int kUnitBytes = kIQ4XSUnit;
     static constexpr int kBlockBytes = kIQ4XSBytes;
@@ -507,6 +525,7 @@ struct IQ4XS {
 // Unit = 4 blocks of 32.  Lane c: block k = c/2 of the unit, half c%2.
 struct Q80 {
     static constexpr uint32_t kType = kQ8_0;
+    static constexpr bool kChunkMajor = false;
     static constexpr int kUnitElems = 128;
     static constexpr int kUnitBytes = kQ80Unit;
     static constexpr int kBlockBytes = kQ80Bytes;
@@ -590,16 +609,42 @@ struct Q80 {
 // cost 3-7 vector instructions per unit).  Measured per kernel (its callers
 // choose): down 0.2 us and the few-token layer 1 us faster with them, the
 // multi-tile Q4_K shapes (config 1, o) 0.2-0.5 us slower.
+// Lane roles of the GEMV kernels (row i of the wave's 8-row tile, 16-byte
+// chunk c of the row's unit) and the sum over the 8 lanes of a row.  With the
+// chunk-pair-first qs plane of TILED Q4_K / Q5_K, lane l reads plane bytes
+// 16 l as row (l / 2) % 8, chunk 2 (l / 16) + l % 2, so a row's lanes are
+// l = 2 i + {0, 1} + {0, 16, 32, 48}.
+template <class T, int LAYOUT>
+struct LaneMap {
+    static constexpr bool kCM = LAYOUT == M27Q_LAYOUT_TILED && T::kChunkMajor;
+    __device__ static int row(int lane) { return kCM ? (lane >> 1) & 7 : lane >> 3; }
+    __device__ static int chunk(int lane) { return kCM ? ((lane >> 4) << 1) | (lane & 1) : lane & 7; }
+    // Every lane of the row gets the sum.
+    __device__ static float sum(float v) {
+        if constexpr (kCM) {
+            v += dpp_f<kDppXor1>(v);
+            // gfx950's row swaps: each sum pairs lane l with l ^ 16, then with l ^ 32
+            const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+            const auto w = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            return __uint_as_float(w[0]) + __uint_as_float(w[1]);
+        } else {
+            return sum8(v);
+        }
+    }
+};
+
 template <class T, int LAYOUT, int NM, int TPW, bool NT = false, bool BUF = true>
 struct UnitStream {
     static constexpr bool kTiled = LAYOUT == M27Q_LAYOUT_TILED, kBuf = kTiled && BUF;
     __amdgpu_buffer_rsrc_t rs[kBuf ? NM : 1][kBuf ? TPW : 1];  // TILED with BUF: one tile each
     const uint8_t *base[NM][TPW];  // TILED: first unit of the tile; GGUF: this lane's row
-    int i, c, rb;
+    int i, c, rb, ln;
     typename T::Lane L;
 
     __device__ UnitStream(const uint8_t *const *W, int tile0, int ntiles, int rc, int rb_, int upr, int lane)
-        : i(lane >> 3), c(lane & 7), rb(rb_), L(lane & 7) {
+        : i(LaneMap<T, LAYOUT>::row(lane)), c(LaneMap<T, LAYOUT>::chunk(lane)), rb(rb_), ln(lane),
+          L(LaneMap<T, LAYOUT>::chunk(lane)) {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -616,6 +661,19 @@ struct UnitStream {
             }
     }
 
+    // Tile t of matrix m only.
+    __device__ void load_tile(typename T::Frag (&f)[NM][TPW], int m, int t, int u) const {
+        if constexpr (kBuf)
+            f[m][t] = T::template load_tiled_buf<NT ? 2 : 0>(rs[m][t], (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
+        else if constexpr (LaneMap<T, LAYOUT>::kCM)
+            f[m][t] = T::template load_tiled_lane<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, ln, i);
+        else if constexpr (kTiled)
+            f[m][t] = T::template load_tiled<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
+        else if constexpr (T::kType == kQ6_K)
+            f[m][t] = T::template load_gguf<NT, TPW == 1>(base[m][t], u, rb, c, L);
+        else
+            f[m][t] = T::template load_gguf<NT>(base[m][t], u, rb, c, L);
+    }
     __device__ void load(typename T::Frag (&f)[NM][TPW], int u) const {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
@@ -624,6 +682,8 @@ struct UnitStream {
                 if constexpr (kBuf)
                     f[m][t] = T::template load_tiled_buf<NT ? 2 : 0>(rs[m][t], (uint32_t)u * (uint32_t)T::kUnitBytes,
                                                                      i, c, L);
+                else if constexpr (LaneMap<T, LAYOUT>::kCM)
+                    f[m][t] = T::template load_tiled_lane<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, ln, i);
                 else if constexpr (kTiled)
                     f[m][t] = T::template load_tiled<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
                 else if constexpr (T::kType == kQ6_K)

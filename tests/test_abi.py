@@ -66,13 +66,17 @@ def test_tiled_layout_offsets(m27q):
     unit = ((r // 8) * rb + b) * 1152
     i = r % 8
     assert np.array_equal(tiled[unit + 16 * i: unit + 16 * i + 16], raw[r, b, :16])
-    assert np.array_equal(tiled[unit + 128 + 128 * i: unit + 256 + 128 * i], raw[r, b, 16:])
+    for g in range(4):  # qs chunk pair g of row i at 128 + 256 g + 32 i
+        assert np.array_equal(tiled[unit + 128 + 256 * g + 32 * i: unit + 160 + 256 * g + 32 * i],
+                              raw[r, b, 16 + 32 * g: 48 + 32 * g])
     t = m27q.Q5_K
     raw = RNG.integers(0, 256, (rc, rb, 176), dtype=np.uint8)
     tiled = m27q.repack(t, rb, rc, raw.reshape(-1))
     unit = ((r // 8) * rb + b) * 1408
     assert np.array_equal(tiled[unit + 16 * i: unit + 16 * i + 16], raw[r, b, :16])
-    assert np.array_equal(tiled[unit + 128 + 128 * i: unit + 256 + 128 * i], raw[r, b, 48:])
+    for g in range(4):
+        assert np.array_equal(tiled[unit + 128 + 256 * g + 32 * i: unit + 160 + 256 * g + 32 * i],
+                              raw[r, b, 48 + 32 * g: 80 + 32 * g])
     assert np.array_equal(tiled[unit + 1152 + 32 * i: unit + 1184 + 32 * i], raw[r, b, 16:48])
     t = m27q.IQ4_XS
     raw = RNG.integers(0, 256, (rc, rb, 136), dtype=np.uint8)

@@ -89,7 +89,7 @@ def test_retile_blob_reads_back_with_the_reference_code(m27q, ref, tmp_path):
         data = tensor_bytes(dst, ref, e_out)
         if t in (12, 13, 14, 8, 23):
             rb = re // m27q.BLOCK_ELEMS[t]
-            assert e_out["reserved"] == m27q.TILED
+            assert e_out["reserved"] == m27q.TILED | TILED_REVISION << 16
             assert e_out["data_bytes"] == m27q.weight_bytes(t, rb, rc, m27q.TILED)
             assert np.array_equal(m27q.unpack(t, rb, rc, data), d), name
         else:
@@ -133,20 +133,37 @@ def test_blob_tensors_match_the_reference_reader(m27q, ref, tmp_path):
         for g, w, (name, t, role, re, rc) in zip(got, want, TENSORS):
             assert g.name == w["name"] and g.ggml_type == w["ggml_type"] and g.role == w["role"]
             assert g.source_model == w["source_model"] and g.row_elems == re and g.row_count == rc
-            assert g.layout == w["reserved"] and g.bytes == w["data_bytes"]
+            assert g.layout == w["reserved"] & 0xffff and g.bytes == w["data_bytes"]
             assert g.file_offset == base + int(w["data_offset"])
             assert g.row_blocks == re // m27q.BLOCK_ELEMS[t]
             assert g.bytes == m27q.weight_bytes(t, g.row_blocks, rc, g.layout)
 
 
-ENTRY_OFF_DATA_OFFSET, ENTRY_OFF_DATA_BYTES = 88, 96
+ENTRY_OFF_RESERVED, ENTRY_OFF_DATA_OFFSET, ENTRY_OFF_DATA_BYTES = 84, 88, 96
+TILED_REVISION = 2  # the TILED byte order with the Q4_K / Q5_K qs plane chunk pair first
 
 
-def _patch_entry(path, ref, i, field_off, value):
+def _patch_entry(path, ref, i, field_off, value, nbytes=8):
     base = ref.refblob_weights_offset(path.encode())
     with open(path, "r+b") as f:
         f.seek(base + 16 + i * ENTRY.itemsize + field_off)
-        f.write(int(value).to_bytes(8, "little"))
+        f.write(int(value).to_bytes(nbytes, "little"))
+
+
+def test_blob_tiled_entry_of_another_revision_is_not_loadable(m27q, ref, tmp_path):
+    """A TILED entry whose reserved field carries another revision of the TILED
+    byte order (here the first, tag 1) is listed with row_blocks 0, which
+    m27q_blob_load refuses, instead of being read in the wrong order."""
+    src, dst = str(tmp_path / "in.m27b"), str(tmp_path / "out.m27b")
+    write_blob(ref, m27q, src, np.random.default_rng(11))
+    m27q.retile_blob(src, dst)
+    ents = read_entries(ref, dst)
+    i = next(k for k, e in enumerate(ents) if e["reserved"] == m27q.TILED | TILED_REVISION << 16)
+    _patch_entry(dst, ref, i, ENTRY_OFF_RESERVED, m27q.TILED, nbytes=4)
+    t = m27q.blob_tensors(dst)[i]
+    assert t.layout == m27q.TILED and t.row_blocks == 0
+    w = m27q.WeightDesc()
+    assert m27q.lib().m27q_blob_load(dst.encode(), C.byref(t), 1 << 20, int(t.bytes), C.byref(w)) == 3
 
 
 @pytest.mark.parametrize("field_off,value", [
