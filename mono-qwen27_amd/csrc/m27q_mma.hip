@@ -30,15 +30,17 @@
 // With PK = 2 each MFMA m covers positions 16 m .. 16 m + 15, which keeps
 // the two Q6_K sub-blocks apart.
 //
-// Data movement.  The operand layouts above would need 8-byte loads that
-// each touch 16 rows (or 16 token rows K bytes apart); measured on gfx950,
-// such loads stall in the L1 tag lookup and bound the kernel well below the
-// HBM rate.  So each wave streams its K slice one TILED unit at a time with
-// 16-byte loads of contiguous bytes (the set's weight tiles, the tokens'
-// codes and scales), issued while the previous unit computes, writes them to
-// its own LDS area (padded row and token records, so the operand reads below
-// are free of bank conflicts), and reads the MFMA operands from there.  The
-// zero operand lanes read a zero record.  K is split over the KS waves of a
+// Data movement.  The operand layouts above would need loads that each touch
+// 16 rows (or 16 token rows K bytes apart); measured on gfx950, such loads
+// stall in the L1 tag lookup and bound the kernel well below the HBM rate.
+// So each wave streams its K slice one TILED unit at a time with 16-byte loads
+// of contiguous bytes (the set's weight tiles, the tokens' codes and scales),
+// issued while the previous unit computes, writes them to its own LDS area
+// (padded row and token records, so the operand reads below are free of bank
+// conflicts), and reads the MFMA operands from there.  TILED Q4_K / Q5_K
+// weights skip that round trip (kDirect): their qs plane is stored chunk pair
+// first, so the operand loads of 16 rows read whole 128-byte lines and go
+// straight into registers.  The zero operand lanes read a zero record.  K is split over the KS waves of a
 // workgroup, one row set per workgroup (two for one-set tiles, sharing the
 // activation operands), and the KS partials are added in LDS in a fixed
 // order.  Padding tokens (past M) read a real token's codes; their
@@ -639,7 +641,10 @@ struct Stage {
 // kernels, for GGUF-layout Q5_K / Q6_K and for Q4_K / Q5_K / Q6_K with two
 // row sets per workgroup, and 2 for GGUF-layout Q6_K with two row sets (185
 // VGPRs with its shifted chunk loads; its 8-wave launches take 104 KB of LDS,
-// so one workgroup per CU runs 2 waves per SIMD in any case).
+// so one workgroup per CU runs 2 waves per SIMD in any case).  With direct
+// operands (TILED Q4_K / Q5_K: the current and the next unit's weights in
+// registers) 3, and 2 for Q5_K with two row sets (187 VGPRs); at 4 the
+// two-set Q4_K kernel spilled 100 bytes per lane.
 template <class T, int PK, int LAYOUT, int RS>
 constexpr int mm_waves_per_eu() {
     if (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2 && RS == 2) return 2;
@@ -944,7 +949,8 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
 // every unit's 16 activation rows in each wave (4.4 KB per unit against
 // 2.3 KB of Q4_K weights for 16 rows); here each workgroup stages the M x K
 // activation codes and scales into LDS once and then streams its share of the
-// row sets' weights through per-wave staging areas as above.
+// row sets' weights through per-wave staging areas as above (TILED Q4_K /
+// Q5_K: straight into registers, as above).
 //
 // LDS: TK token records of Kp + 16 bytes (Kp = the units' K; the 16-byte pad
 // keeps the token stride at 16 mod 128 bytes, as the per-unit records'), a
@@ -983,6 +989,7 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
     using XS = XStage<T>;
     using SG = typename XS::SG;
     constexpr bool kG = LAYOUT == M27Q_LAYOUT_GGUF;  // as in k_matmul_mfma
+    constexpr bool kD = !kG && T::kDirect;            // weight operands straight into registers
     static_assert(!kG || 16 * T::kGgufChunks <= SG::kNW * kWave, "GGUF chunks fit the staging registers");
     constexpr int G = T::kGroups, NS = T::kSteps, TK = 16, UE = SG::UE, UB = SG::UB;
     constexpr int CPU = UB / 16;
@@ -1063,6 +1070,7 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
     v4u rw[SG::kNW];
     uint32_t re[kA2 ? SG::kNW : 1], rsh[kA2 ? SG::kNW : 1], rd = 0u;
     auto issue = [&](int idx) __attribute__((always_inline)) {
+        if constexpr (kD) return;
         const int gs = s0 + idx / upr, u = idx % upr;
         int mi = 0;
 #pragma unroll
@@ -1098,7 +1106,8 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
         }
     };
     auto commit = [&]() __attribute__((always_inline)) {
-        if constexpr (kA2) {
+        if constexpr (kD) {
+        } else if constexpr (kA2) {
 #pragma unroll
             for (int n = 0; n < SG::kNW; ++n) *(v4u *)(wl + wdst[n]) = shift16(rw[n], re[n], rsh[n]);
             *(uint16_t *)(wl + ddst) = (uint16_t)rd;
@@ -1110,6 +1119,21 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
 
     const int wrow = L.c;  // the lane's weight row within the set
     const int atok = L.c;  // and its token
+    // Direct operands of unit idx of the run: row wrow of its set.
+    typename T::template Direct<1> dc, dn;
+    auto dload = [&](int idx, typename T::template Direct<1> &d) __attribute__((always_inline)) {
+        if constexpr (kD) {
+            const int gs = s0 + idx / upr, u = idx % upr;
+            int mi = 0;
+#pragma unroll
+            for (int k = 1; k < kMaxMulti; ++k)
+                if (k < p.nmat && gs >= p.wg_start[k]) mi = k;
+            const int ntiles8 = (p.rc[mi] + kTileRows - 1) / kTileRows;
+            const __amdgpu_buffer_rsrc_t wr = buf_rsrc(p.W[mi], (uint32_t)ntiles8 * (uint32_t)(upr * UB));
+            const int tile = min((gs - p.wg_start[mi]) * 2 + (wrow >> 3), ntiles8 - 1);
+            T::template load_direct<1>(d, wr, (uint32_t)tile * (uint32_t)(upr * UB), wrow & 7, L.r, (uint32_t)u * UB);
+        }
+    };
     const uint8_t *xa = X + atok * xrow + 8 * L.r;
     const uint8_t *xz = smem + XS::oZero(upr) + 8 * L.r;
     const ScaleLds<1> sl{dT, aT};
@@ -1126,10 +1150,16 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
         }
         typename T::template Frag<1> f0, f1;
         AFrag<NP> x0, x1;
-        T::template load<1>(f0, wl, wrow, L.r, 0, SG::kSide);
+        if constexpr (kD)
+            T::template frag_direct<1>(f0, dc, 0);
+        else
+            T::template load<1>(f0, wl, wrow, L.r, 0, SG::kSide);
         load_act<NP>(x0, ab, 0);
         if constexpr (NS == 2) {
-            T::template load<1>(f1, wl, wrow, L.r, 1, SG::kSide);
+            if constexpr (kD)
+                T::template frag_direct<1>(f1, dc, 1);
+            else
+                T::template load<1>(f1, wl, wrow, L.r, 1, SG::kSide);
             load_act<NP>(x1, ab, 1);
         }
         compute_half<T, 1, 0>(f0, x0, sl, u * G, L, true, atok, acc, u4, cm);
@@ -1145,7 +1175,10 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
         cm = v4f{0.f, 0.f, 0.f, 0.f};
     };
     // The first unit's weights load while the activation staging completes.
-    if (ua < ub) issue(ua);
+    if (ua < ub) {
+        issue(ua);
+        dload(ua, dc);
+    }
     __syncthreads();
 
     // 3. The run, one unit ahead as in the kernel above (unconditional loads,
@@ -1155,9 +1188,11 @@ __global__ __launch_bounds__(kWave *NWV, 1) void k_matmul_mfma_xres(MatmulMultiP
         commit();
         for (int k = 0; k + 1 < ub - ua; ++k) {
             issue(ua + k + 1);
+            dload(ua + k + 1, dn);
             compute(ua + k);
             if (k + 1 == n_first) close_first();
             commit();
+            if constexpr (kD) dc = dn;
         }
         compute(ub - 1);
         if (ub - ua == n_first) {
@@ -1256,12 +1291,13 @@ static bool launch_xres_t(MatmulMultiParams p, int m0, hipStream_t s, hipError_t
     return true;
 }
 // GGUF-layout Q6_K's shifted chunk loads do not fit the resident kernel's 128
-// registers without spilling: those launches take the per-unit kernel.  So do
-// TILED Q4_K / Q5_K, whose per-unit kernel loads the weight operands straight
-// into registers: gate/up at M = 16 31.4 us against 32.9 resident.
+// registers without spilling: those launches take the per-unit kernel.
+// TILED Q4_K / Q5_K take it with their weight operands loaded straight into
+// registers (gate/up at M = 16: 29.4 us against 31.8 on the per-unit kernel
+// with direct operands and 30.5 resident with staged weights, same box).
 template <class T, int LAYOUT>
 static bool launch_xres(const MatmulMultiParams &p, int m0, hipStream_t s, hipError_t *err) {
-    if constexpr ((LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2) || (LAYOUT == M27Q_LAYOUT_TILED && T::kDirect))
+    if constexpr (LAYOUT == M27Q_LAYOUT_GGUF && T::kGgufA2)
         return false;
     else
         return launch_xres_t<T, LAYOUT>(p, m0, s, err);
@@ -1293,6 +1329,11 @@ constexpr int kPk2MinSets = 128;
 // spills at 12 waves and keeps 8).  The same for Q4_K's q/k/v and o was
 // slower at M <= 8 (q/k/v 7.5 against 7.2 us) and equal at M = 16.
 constexpr long long kQ6Wide12MaxWgs = 256;
+// Two-set tiles with direct operands (TILED Q4_K / Q5_K, 155-168 VGPRs, 3
+// waves per SIMD) in launches of 320 or more workgroups split K over 4 waves,
+// so three workgroups share a CU: gate/up at M = 4 / 8 21.5 / 22.2 us against
+// 25.0 / 25.9 with 8 waves (one workgroup per CU), 22.1 / 23.4 with 2; q/k/v
+// and o (256 and 160 workgroups) keep 8: 6.6 / 6.8 us against 7.4 / 7.7 with 4.
 constexpr long long kDirectKs4MinWgs = 320;
 template <class T, int PK, int LAYOUT>
 static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t s) {
