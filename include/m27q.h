@@ -63,8 +63,9 @@ enum {
  *         the reference uploads them (exec:1695-1716).
  *  TILED: the pack-time re-tiling produced by m27q_repack.  Rows are grouped in
  *         tiles of 8; within a tile, each block column is stored plane by plane
- *         (headers, then quants) so that one wavefront load instruction reads
- *         1 KiB of contiguous bytes.  Byte-preserving per block, 16-byte aligned,
+ *         (headers, then quants; the Q4_K / Q5_K quants by 32-byte chunk pair,
+ *         then row) so that one wavefront load instruction reads 1 KiB of
+ *         contiguous bytes.  Byte-preserving per block, 16-byte aligned,
  *         inverted exactly by m27q_unpack. */
 enum { M27Q_LAYOUT_GGUF = 0, M27Q_LAYOUT_TILED = 1 };
 
