@@ -719,7 +719,29 @@ __global__ __launch_bounds__(kWave *KS, (mm_waves_per_eu<T, PK, LAYOUT, RS>())) 
             wdst[n] = ok ? T::gguf_dst(j, c) : SG::oDummy;
         } else {
             const bool ok = id < SG::kWChunks;
-            const int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
+            int t = ok ? id / CPU : 0, c = ok ? id % CPU : 0;
+            if constexpr (std::is_same<T, MmQ6K>::value) {
+                // Q6_K's 240-byte records: each 16-lane pass of the staging
+                // writes takes rows whose records fall on distinct banks (the
+                // same row of two adjacent tiles for ql, rows i, i + 4 of two
+                // tiles for qh), 8 or 4 lanes still reading a row's whole
+                // 128 / 64 bytes.  Down at M = 4: 20.6 us against 21.2 with
+                // consecutive chunks.
+                constexpr int NT = SG::kWChunks / CPU;
+                if (ok && id < 64 * NT) {
+                    const int pp = id >> 4, j = id & 15;
+                    t = 2 * (pp >> 3) + (j >> 3);
+                    c = 8 * (pp & 7) + (j & 7);
+                } else if (ok && id < 96 * NT) {
+                    const int q = id - 64 * NT, pp = q >> 4, j = q & 15, sub = j >> 2;
+                    t = 2 * (pp >> 2) + (sub >> 1);
+                    c = 64 + 4 * ((pp & 3) + 4 * (sub & 1)) + (j & 3);
+                } else if (ok) {
+                    const int q = id - 96 * NT;
+                    t = q / 9;
+                    c = 96 + q % 9;
+                }
+            }
             const int tile = min(row0 / kTileRows + t, ntiles8 - 1);
             goff[n] = (uint32_t)tile * (uint32_t)(p.upr * UB) + 16u * c;
             wdst[n] = ok ? T::lds_dst(t, c, SG::kSide) : SG::oDummy;
@@ -1327,7 +1349,11 @@ constexpr int kPk2MinSets = 128;
 // 22.5 / 23.1, at M = 12 / 16 25.5 / 26.8 against 26.9 / 28.2 (GGUF layout
 // at M <= 8 unchanged, 26.9 / 27.6 against 26.8 / 27.8; its one-set kernel
 // spills at 12 waves and keeps 8).  The same for Q4_K's q/k/v and o was
-// slower at M <= 8 (q/k/v 7.5 against 7.2 us) and equal at M = 16.
+// slower at M <= 8 (q/k/v 7.5 against 7.2 us) and equal at M = 16 with
+// staged weights; with direct operands (one workgroup per CU at 3 waves per
+// SIMD) the one-set launches gain: at M = 16 q/k/v 8.6 against 9.2 us, o 9.3
+// against 10.0, while two-set ones lose (q/k/v 6.9 against 6.7 at M = 4).
+// Q5_K with two row sets needs 187 VGPRs and spills at 12 waves.
 constexpr long long kQ6Wide12MaxWgs = 256;
 // Two-set tiles with direct operands (TILED Q4_K / Q5_K, 155-168 VGPRs, 3
 // waves per SIMD) in launches of 320 or more workgroups split K over 4 waves,
@@ -1348,7 +1374,7 @@ static hipError_t launch_mfma_pk(const MatmulMultiParams &p, int m0, hipStream_t
             if (wgs >= kDirectKs4MinWgs) return launch_mfma_t<T, 2, 4, LAYOUT, RS>(p, m0, s);
         return launch_mfma_t<T, 2, 8, LAYOUT, RS>(p, m0, s);
     } else {
-        if constexpr (std::is_same<T, MmQ6K>::value && LAYOUT == M27Q_LAYOUT_TILED)
+        if constexpr ((std::is_same<T, MmQ6K>::value || (T::kDirect && !T::kWide)) && LAYOUT == M27Q_LAYOUT_TILED)
             if (wgs <= kQ6Wide12MaxWgs) return launch_mfma_t<T, 1, 12, LAYOUT, RS>(p, m0, s);
         const int ks = wgs < 320 ? 8 : 4;
         return ks == 8 ? launch_mfma_t<T, 1, 8, LAYOUT, RS>(p, m0, s) : launch_mfma_t<T, 1, 4, LAYOUT, RS>(p, m0, s);
