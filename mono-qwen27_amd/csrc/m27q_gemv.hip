@@ -465,10 +465,6 @@ static hipError_t launch_q8_t(const GemvParams &p, int cfg, hipStream_t s) {
         case kCfg161:  // chosen for small products without the SwiGLU epilogue only
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, Cfg161, SWIGLU, XF32>(p, s);
             return launch_q8_cfg<T, LAYOUT, Cfg41, SWIGLU, XF32>(p, s);
-        case kCfg822:  // fp32-input products without the SwiGLU epilogue only; the
-                       // other instantiation keeps the tiles per workgroup the grid was sized for
-            if constexpr (!SWIGLU && XF32) return launch_q8_cfg<T, LAYOUT, Cfg822, SWIGLU, XF32>(p, s);
-            return launch_q8_cfg<T, LAYOUT, Cfg42, SWIGLU, XF32>(p, s);
         case kCfgB:  // balanced tiling, single products without the SwiGLU epilogue only
             if constexpr (!SWIGLU) return launch_q8_cfg<T, LAYOUT, CfgB, SWIGLU, XF32>(p, s);
             return hipErrorInvalidValue;
@@ -505,7 +501,6 @@ static size_t lds_for(int upr, bool swiglu, int cfg) {
         case kCfg84: return lds_sw<T, Cfg84>(upr, swiglu);
         case kCfgQ: return lds_sw<T, CfgQ>(upr, swiglu);
         case kCfg161: return swiglu ? lds_sw<T, Cfg41>(upr, swiglu) : lds_sw<T, Cfg161>(upr, swiglu);
-        case kCfg822: return std::max(lds_sw<T, Cfg42>(upr, swiglu), lds_sw<T, Cfg822>(upr, swiglu));
         case kCfgB: return lds_sw<T, CfgB>(upr, swiglu);
         case kCfgB9: return lds_sw<T, CfgB9>(upr, swiglu);
         default: return lds_sw<T, Cfg41>(upr, swiglu);
@@ -530,7 +525,6 @@ int gemv_q8_tiles_per_wg(int cfg) {
         case kCfg84: return Cfg84::TPW;
         case kCfgQ: return CfgQ::TPW;
         case kCfg161: return Cfg161::TPW;
-        case kCfg822: return Cfg822::TPW;
         case kCfgB: return CfgB::TPW;
         case kCfgB9: return CfgB9::TPW;
         default: return Cfg41::TPW;

@@ -29,6 +29,9 @@
 //     7.8 against 8.4)
 //   o 5120 x 6144 Q4_K                       (8,2,2) 7.51 us     (8,1) 6.01 us
 //                                            (8,1) 7.88, (6,2,1) 7.98, (4,2,2) 8.24
+//     (with the chunk-pair-first qs plane, in graphs of 32 launches:
+//     (8,4,2) 6.23, (8,1,1) 6.28, (8,2,2) 6.59, (16,1,1) 7.42, (4,2,2) 7.63;
+//     the layer 46.09 against 46.28 us with (8,4,2), median of six rounds)
 //   gate/up SwiGLU 2 x 17408 x 5120 Q4_K     (4,1) 20.91 us      (8,1) 20.19 us
 //   down 5120 x 17408 Q6_K                   (4,1) 21.30 us      (4,1) 17.09 us
 //   gate/up + fused output quantization      (2,4,2) 24.2 us (2,4,1) 24.85, (4,4,4) 24.4,
@@ -82,15 +85,14 @@ using Cfg42 = GemvCfg<4, 2, 2, 1>;
 using Cfg84 = GemvCfg<8, 4, 2, 0>;
 using CfgQ = GemvCfg<2, 4, 2, 1>;
 using Cfg161 = GemvCfg<16, 1, 1, 1>;
-using Cfg822 = GemvCfg<8, 2, 2, 0>;
 using CfgB = GemvCfg<4, 3, 1, 1>;  // balanced tiling (GemvParams::bal), up to TPW tiles per workgroup
 using CfgB9 = GemvCfg<5, 9, 3, 1>;  // balanced tiling for 8-9 tiles per CU (config 1); swept against
                                      // (4, 9, 3) +0.3, (3, 9, 3) +0.5, (8, 9, 9) +0.4, (4, 9, 9) +1.8,
                                      // (2, 9, 3) +1.5 us
 static_assert(CfgQ::TPW * 8 % 32 == 0, "output-quantizing workgroups hold whole 32-row groups");
-static_assert(Cfg822::TPW == Cfg42::TPW && Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
+static_assert(Cfg161::TPW == Cfg41::TPW, "a fallback instantiation keeps the grid's tiles per workgroup");
 
-enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfg822 = 6, kCfgB = 7, kCfgB9 = 8 };
+enum { kCfg41 = 0, kCfg81 = 1, kCfg42 = 2, kCfg84 = 3, kCfgQ = 4, kCfg161 = 5, kCfgB = 7, kCfgB9 = 8 };
 
 // Host-side choice for a product of rows_total output rows (all matrices of a
 // multi-matrix launch) of one weight type and layout over upr units per row.
@@ -107,7 +109,7 @@ inline int pick_gemv_cfg(uint32_t type, bool tiled, bool xf32, bool swiglu, bool
     if (swiglu) return upr >= 40 || xf32 ? kCfg41 : kCfg81;
     if (upr >= 40) return rows_total <= 4096 ? kCfg161 : kCfg41;
     if (rows_total <= 12288) {
-        if (upr >= 24) return xf32 ? (tiled ? kCfg822 : kCfg41) : kCfg81;
+        if (upr >= 24) return xf32 ? (tiled ? kCfg84 : kCfg41) : kCfg81;
         if (!xf32) return kCfg41;
         if (rows_total <= 2048) return kCfg161;
         if (rows_total <= 6144) return kCfg81;
