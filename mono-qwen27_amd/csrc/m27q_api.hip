@@ -205,7 +205,11 @@ m27q_status gemv_impl(int n, const m27q_weight *ws, const void *xq, const float 
 // streaming structure when their activations fit the LDS budget
 // (m27q_gemv_mt.hip), otherwise on int8 MFMA (m27q_mma.hip).  Measured on the
 // Qwen-27B layer: 56 us against 63 at M = 2; from M = 3 on the MFMA kernel
-// with two row sets per tile is faster (63 against 75 us at M = 4).
+// with two row sets per tile is faster (63 against 75 us at M = 4).  TILED
+// Q4_K / Q5_K, whose MFMA kernel loads the weight operands straight into
+// registers, take it from M = 2: q/k/v 6.5 against 9.1 us, o 6.5 against
+// 7.8, gate/up 20.5 against 21.6 (Q6_K down keeps the GEMV structure: 17.7
+// against 20.1 on MFMA).
 // GGUF-layout weights take the same few-token kernel (with temporal loads);
 // from M = 3, GGUF-layout Q4_K / Q5_K / Q6_K take the MFMA kernel (staged from
 // the row blocks), GGUF-layout Q8_0 and IQ4_XS one launch per matrix of the
@@ -233,7 +237,8 @@ m27q_status matmul_multi_impl(int n, const m27q_weight *ws, int M, const void *x
     p.K = k_of(&ws[0]);
     p.M = M;
     const ActView a = act_view(xq, M, p.K);
-    const bool few = M <= kMtMaxM && matmul_mt_lds_bytes(type, p.upr) <= kMtLdsBudget;
+    const bool few = M <= kMtMaxM && (M == 1 || !matmul_mfma_direct(type, layout)) &&
+                     matmul_mt_lds_bytes(type, p.upr) <= kMtLdsBudget;
     if (!few && !matmul_mfma_takes(type, layout)) {  // GGUF Q8_0 / IQ4_XS from M = 3
         if (dry) return M27Q_OK;
         for (int i = 0; i < n; ++i) {

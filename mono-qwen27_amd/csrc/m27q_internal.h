@@ -114,6 +114,8 @@ hipError_t launch_matmul_mt(uint32_t type, int layout, const MatmulMultiParams &
 // launch).
 size_t matmul_mfma_lds_bytes(uint32_t type);
 bool matmul_mfma_takes(uint32_t type, int layout);
+// Whether its weight operands go straight into registers (TILED Q4_K / Q5_K).
+bool matmul_mfma_direct(uint32_t type, int layout);
 // The current device's CU count and LDS bytes per workgroup (cached per device).
 int cu_count();
 size_t lds_limit();

@@ -1423,6 +1423,10 @@ bool matmul_mfma_takes(uint32_t type, int layout) {
     return layout == M27Q_LAYOUT_TILED || type == kQ4_K || type == kQ5_K || type == kQ6_K;
 }
 
+bool matmul_mfma_direct(uint32_t type, int layout) {
+    return layout == M27Q_LAYOUT_TILED && (type == kQ4_K || type == kQ5_K);
+}
+
 hipError_t launch_matmul_mfma(uint32_t type, int layout, const MatmulMultiParams &p, hipStream_t s) {
     if (layout == M27Q_LAYOUT_GGUF) {
         switch (type) {
