@@ -597,18 +597,6 @@ struct Q80 {
     }
 };
 
-// ------------------------------------------------------- weight stream --
-// Weight fragments of one unit for the TPW tiles of every matrix (the caller
-// includes m27q.h for the layout tags).  NT selects non-temporal 16-byte loads
-// (ld_u128<true>); the GGUF blocks that are only 2- or 8-byte aligned (Q6_K,
-// Q8_0, IQ4_XS) are read in smaller pieces and keep the default policy.
-// With BUF, TILED weights are read through one buffer descriptor per tile
-// (its base and byte count in scalar registers): the plane offsets of the
-// lane are one loop-invariant register and the unit's offset a scalar, so a
-// load costs no vector address arithmetic (with 64-bit per-lane addresses it
-// cost 3-7 vector instructions per unit).  Measured per kernel (its callers
-// choose): down 0.2 us and the few-token layer 1 us faster with them, the
-// multi-tile Q4_K shapes (config 1, o) 0.2-0.5 us slower.
 // Lane roles of the GEMV kernels (row i of the wave's 8-row tile, 16-byte
 // chunk c of the row's unit) and the sum over the 8 lanes of a row.  With the
 // chunk-pair-first qs plane of TILED Q4_K / Q5_K, lane l reads plane bytes
@@ -634,6 +622,18 @@ struct LaneMap {
     }
 };
 
+// ------------------------------------------------------- weight stream --
+// Weight fragments of one unit for the TPW tiles of every matrix (the caller
+// includes m27q.h for the layout tags).  NT selects non-temporal 16-byte loads
+// (ld_u128<true>); the GGUF blocks that are only 2- or 8-byte aligned (Q6_K,
+// Q8_0, IQ4_XS) are read in smaller pieces and keep the default policy.
+// With BUF, TILED weights are read through one buffer descriptor per tile
+// (its base and byte count in scalar registers): the plane offsets of the
+// lane are one loop-invariant register and the unit's offset a scalar, so a
+// load costs no vector address arithmetic (with 64-bit per-lane addresses it
+// cost 3-7 vector instructions per unit).  Measured per kernel (its callers
+// choose): down 0.2 us and the few-token layer 1 us faster with them, the
+// multi-tile Q4_K shapes (config 1, o) 0.2-0.5 us slower.
 template <class T, int LAYOUT, int NM, int TPW, bool NT = false, bool BUF = true>
 struct UnitStream {
     static constexpr bool kTiled = LAYOUT == M27Q_LAYOUT_TILED, kBuf = kTiled && BUF;
@@ -661,19 +661,6 @@ struct UnitStream {
             }
     }
 
-    // Tile t of matrix m only.
-    __device__ void load_tile(typename T::Frag (&f)[NM][TPW], int m, int t, int u) const {
-        if constexpr (kBuf)
-            f[m][t] = T::template load_tiled_buf<NT ? 2 : 0>(rs[m][t], (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
-        else if constexpr (LaneMap<T, LAYOUT>::kCM)
-            f[m][t] = T::template load_tiled_lane<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, ln, i);
-        else if constexpr (kTiled)
-            f[m][t] = T::template load_tiled<NT>(base[m][t] + (uint32_t)u * (uint32_t)T::kUnitBytes, i, c, L);
-        else if constexpr (T::kType == kQ6_K)
-            f[m][t] = T::template load_gguf<NT, TPW == 1>(base[m][t], u, rb, c, L);
-        else
-            f[m][t] = T::template load_gguf<NT>(base[m][t], u, rb, c, L);
-    }
     __device__ void load(typename T::Frag (&f)[NM][TPW], int u) const {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
