@@ -83,7 +83,7 @@ def test_q8_path_no_worse_than_q8K_cpu_path(m27q, ora, dev, type_name, rc, k):
     e_gpu = np.sqrt(np.mean((got - exact) ** 2))
     e_cpu = np.sqrt(np.mean((cpu - exact) ** 2))
     print(f"rms err gpu(per-32 int8)={e_gpu:.3e} cpu(q8_K/q8_0)={e_cpu:.3e} ratio={e_gpu / e_cpu:.3f}")
-    # north_star: no worse than the reference's own q8_K-activation path
+    # the accuracy bar: no worse than the reference's own q8_K-activation path
     assert e_gpu <= e_cpu, f"rms error ratio gpu/cpu = {e_gpu / e_cpu:.4f}"
 
 
