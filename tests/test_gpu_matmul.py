@@ -14,8 +14,9 @@ CASES = [  # type, rows, K, M, layout
     ("Q4_K", 40, 512, 5, 0), ("Q4_K", 40, 512, 64, 1),
     ("Q6_K", 5120, 17408, 16, 1), ("Q6_K", 5120, 17408, 3, 0), ("Q6_K", 24, 768, 9, 1),
     ("Q8_0", 2048, 6144, 16, 1), ("Q8_0", 2048, 6144, 2, 0), ("Q8_0", 13, 160, 7, 1),
-    # few tokens: M = 2 on the GEMV-structured kernel, M = 3 and 4 on MFMA
-    # (padding tokens, partial 8-row tiles), each type
+    # few tokens: M = 2 on the GEMV-structured kernel (TILED Q4_K / Q5_K: on
+    # MFMA with direct weight operands), M = 3 and 4 on MFMA (padding tokens,
+    # partial 8-row tiles), each type
     ("Q6_K", 5120, 17408, 2, 1), ("Q6_K", 24, 768, 4, 1), ("Q4_K", 40, 512, 3, 1), ("Q8_0", 13, 160, 3, 1),
     ("Q8_0", 2048, 6144, 4, 1),
     # Q5_K on each path: few-token GEMV, MFMA, GGUF VALU
@@ -32,10 +33,13 @@ CASES = [  # type, rows, K, M, layout
     # gate-sized rows at M = 3 (two sets per tile), the down shape at M = 12
     # (padding tokens in a 16-token launch), 17 tokens (16, then 1 on two sets)
     ("Q4_K", 17408, 5120, 3, 1), ("Q6_K", 5120, 17408, 12, 1), ("Q4_K", 8192, 512, 17, 1),
-    # few tokens with balanced tiling on 256 CUs (rows under 40 units): o (640
-    # tiles), and both ends of the range with a ragged last tile (513 and 768
-    # tiles)
+    # few tokens with balanced tiling on 256 CUs (rows under 40 units) on the
+    # GEMV-structured kernel (Q6_K), and the same shapes on MFMA with direct
+    # operands (Q4_K): o, a ragged last tile
     ("Q4_K", 5120, 6144, 2, 1), ("Q6_K", 4100, 2048, 2, 1), ("Q4_K", 6141, 2048, 2, 1),
+    # direct weight operands at M = 2: a single partial tile, a partial last
+    # two-set tile, and gate-sized rows (544 workgroups: K over 4 waves)
+    ("Q4_K", 13, 256, 2, 1), ("Q5_K", 8200, 512, 2, 1), ("Q4_K", 17408, 1024, 2, 1),
     # resident activation rows (16-token launches with >= 4 row sets per CU:
     # 1025 sets of 16 rows on 256 CUs), every type, a partial last set, a
     # partial Q8_0 unit (K = 1056), and 16 + 9 tokens (the resident launch,
